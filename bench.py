@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Decode throughput of the 3B AR model at batch 1, KV length 4096, on one GPU.
+
+Workload: the BASELINE 3B decoder (hidden 3072, 24/8 heads, head_dim 128, FFN
+8192, 28 layers, vocab 83968, RMSNorm eps 1e-5, RoPE theta 5e5), random-init
+bf16 weights N(0, 0.02) with unit norm gains, a random prompt prefilled so
+that the timed steps are centred on KV length 4096, then greedy decoding. A
+step is one token: the device sampler (argmax) followed by the whole decode
+step (28 x [QKV GEMV, split-K attention, O GEMV, gate/up GEMV, down GEMV],
+lm_head GEMV), replayed as one hipGraph per token with no host sync between
+tokens. Inputs (weights, KV cache, logits) are resident in HBM when the timed
+region starts.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "yue2-mlx_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+CONFIG = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
+              num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=83968,
+              max_position_embeddings=24576, rms_norm_eps=1e-5, rope_theta=500000.0,
+              qk_norm=True)
+PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+KV_BYTES_PER_POS = 2 * 8 * 128 * 2 * 28  # K and V, Hkv * D * bf16 * layers
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def weight_bytes(c):
+    H, F, V, L = c["hidden_size"], c["intermediate_size"], c["vocab_size"], c["num_hidden_layers"]
+    qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
+    per_layer = (qd + 2 * kd) * H + H * qd + 2 * F * H + H * F  # linear weights
+    return 2 * (L * per_layer + V * H)  # + lm_head (the embedding row gather is 6 KiB)
+
+
+def kernel_bytes(c, kernel, kv_len):
+    """Algorithmic HBM bytes of one launch (weights + activations + KV)."""
+    H, F, V = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
+    qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
+    return {
+        "qkv": 2 * ((qd + 2 * kd) * H + H + (qd + 2 * kd)),
+        "attention": kv_len * 2 * kd * 2 + 2 * (qd + 2 * kd + qd) + 2 * 2 * kd,
+        "o_proj": 2 * (H * qd + qd + 2 * H),
+        "gate_up": 2 * (2 * F * H + H + F),
+        "down": 2 * (H * F + F + 2 * H),
+        "lm_head": 2 * (V * H + H + V),
+    }[kernel]
+
+
+def traffic_from_profiles(kernel):
+    """Measured HBM bytes per launch, if a PMC summary has been committed."""
+    path = os.path.join(ROOT, "profiles", f"gemv_{kernel}_3b_pmc.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--kv", type=int, default=4096)
+    ap.add_argument("--seed", type=int, default=20251201)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-launches", type=int, default=112)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md for how the decode step would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import yuear
+
+    t_start = time.perf_counter()
+    c = CONFIG
+    log(f"[bench] generating 3B weights on host ({weight_bytes(c) / 1e9:.2f} GB) ...")
+    weights = yuear.random_weights(c, args.seed)
+    log(f"[bench] weights ready {time.perf_counter() - t_start:.1f}s; uploading")
+    engine = yuear.Engine(c, weights)
+    W, K = args.warmup, args.steps
+    prefill = args.kv - 1 - W - (K - 1) // 2  # timed steps centred on KV length kv
+    capacity = prefill + W + K + 8
+    session = engine.session(1, capacity)
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, c["vocab_size"], size=prefill).tolist()
+    t = time.perf_counter()
+    session.prefill(0, prompt)
+    torch.cuda.synchronize()
+    log(f"[bench] prefill {prefill} tokens {time.perf_counter() - t:.2f}s")
+
+    greedy = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                  penalty_window=50, min_tokens=0, max_tokens=K + W + 8)
+    session.time_generate(greedy, args.seed, W, reset=True)  # warmup (captures the graph)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dev_ms, tokens = session.time_generate(greedy, args.seed, K, reset=False)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = 1e3 * wall / K
+    value = K / wall
+    mean_kv = prefill + W + (K - 1) / 2 + 1
+    step_bytes = weight_bytes(c) + mean_kv * KV_BYTES_PER_POS
+    log(f"[bench] decode {K} steps: {ms_per_step:.4f} ms/token wall, {dev_ms:.4f} ms device, "
+        f"{value:.1f} tok/s, step roofline {step_bytes / (ms_per_step / 1e3) / PEAK_HBM:.3f}")
+
+    # per-kernel device time (HIP events on the session stream)
+    kernels = {}
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head"):
+        launches = args.kernel_launches if name != "lm_head" else max(8, args.kernel_launches // 8)
+        ms = session.time_kernel(name, launches)
+        nbytes = kernel_bytes(c, name, session.position(0) + 1)
+        kernels[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+                         "GBps": round(nbytes / (ms / 1e3) / 1e9, 1)}
+        log(f"[bench] {name:9s} {ms * 1e3:8.2f} us  {nbytes / 1e6:8.2f} MB  "
+            f"{nbytes / (ms / 1e3) / 1e9:7.1f} GB/s")
+    dom = kernels["gate_up"]
+    achieved = dom["bytes"] / (dom["us"] / 1e6) / 1e9
+    roofline = {"kernel": "gemv_kernel<1,6,2,SwiGLU> (gate/up 16384x3072 + RMSNorm + SwiGLU)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": round(achieved / (PEAK_HBM / 1e9), 4),
+                "traffic": traffic_from_profiles("gate_up")}
+
+    cpu = None
+    if not args.no_cpu:
+        import cpu_ref
+        threads = min(16, os.cpu_count() or 1)
+        if "OMP_NUM_THREADS" in os.environ:
+            threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+        cpu_ref.lib().oracle_set_threads(threads)
+        model = cpu_ref.Model(c, weights)
+        L0 = args.kv - 1
+        cache = model.cache(L0 + 64)
+        for layer in range(c["num_hidden_layers"]):
+            k, v = session.read_kv(layer, 0, L0)
+            cache.keys(layer)[:, :L0] = k
+            cache.values(layer)[:, :L0] = v
+        cache.offset = L0
+        token, n = int(tokens[-1]), 0
+        t = time.perf_counter()
+        while n < 60 and (n < 2 or time.perf_counter() - t < args.cpu_seconds):
+            logits = model.step(token, cache)
+            token = int(cpu_ref.bf16_to_f32(logits).argmax())
+            n += 1
+        elapsed = time.perf_counter() - t
+        cpu = {"value": round(n / elapsed, 4), "unit": "tokens/s", "cores": threads,
+               "kind": "port",
+               "sample": f"{n} greedy decode steps of the same 3B model on the same weights, "
+                         f"KV {L0 + 1}..{L0 + n} copied from the GPU run "
+                         f"(CPU restatement of the reference graph, {elapsed:.1f} s)"}
+        log(f"[bench] cpu oracle {n} steps {elapsed:.1f}s -> {n / elapsed:.3f} tok/s "
+            f"({threads} threads)")
+
+    line = {
+        "metric": "decode tokens/sec @ batch 1, 3B bf16, KV 4096; % of HBM roofline",
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights, unit norm gains, random prompt ids",
+        "config": {"workload": "3B bf16 AR decoder (H3072/F8192/28L/24:8 heads/V83968), "
+                               "greedy decode at batch 1 centred on KV length 4096",
+                   "batch": 1, "kv_len": args.kv, "prefill_tokens": prefill,
+                   "mean_kv_len": mean_kv, "parallelism": "single-gpu"},
+        "step_roofline": {"bytes_per_step": int(step_bytes),
+                          "achieved_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
+                          "frac": round(step_bytes / (ms_per_step / 1e3) / PEAK_HBM, 4),
+                          "device_ms_per_step": round(dev_ms, 5)},
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    log(f"[bench] total {time.perf_counter() - t_start:.1f}s")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,220 @@
+/*
+ * yuear.h — C ABI of the gfx950 (MI355X) autoregressive decode library.
+ *
+ * Drop-in boundary for the reference's AR decode loop. The reference engine
+ * API it replaces is native/include/lyra/ar.hpp:8-48 (ARModel, KVCache,
+ * generate_tokens), whose only caller is Pipeline::generate_phase
+ * (native/src/pipeline.cpp:186-211); the GraphAR decode-step pattern it
+ * mirrors is vendor/yue/src/yue2/cuda_graph.py:35-240. ABI conventions follow
+ * native/include/CLyraCore/lyra.h:8-54: opaque handles, UTF-8 JSON for results
+ * and errors, caller-owned output strings freed with yuear_string_free, status
+ * codes 0/1/2/130, no exception crosses the boundary, one call at a time per
+ * handle, synchronous execution on the calling thread.
+ *
+ * All bf16 data crossing the boundary is passed as uint16_t bit patterns.
+ * Host pointers unless a name says `dev_` (device pointers, for the op-level
+ * entry points that mirror the reference's model_ops namespace).
+ */
+#ifndef YUEAR_H
+#define YUEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* lyra.h:18-23 */
+typedef enum yuear_status {
+  YUEAR_SUCCESS = 0,
+  YUEAR_FAILURE = 1,
+  YUEAR_INVALID_INPUT = 2,
+  YUEAR_CANCELLED = 130
+} yuear_status;
+
+/* Architectural config (the fields ar.cpp:164-192 validates). */
+typedef struct yuear_model_config {
+  int32_t hidden_size, intermediate_size, num_hidden_layers;
+  int32_t num_attention_heads, num_key_value_heads, head_dim;
+  int32_t vocab_size, max_position_embeddings;
+  float rms_norm_eps;
+  double rope_theta;
+  int32_t qk_norm; /* 1 = Qwen3 per-head q/k RMSNorm (ar.cpp:268-275) */
+} yuear_model_config;
+
+/* Sampling, native/include/lyra/types.hpp:29-38. */
+typedef struct yuear_sampling {
+  double temperature, top_p;
+  int32_t top_k;
+  double repetition_penalty;
+  int32_t penalty_window, min_tokens, max_tokens;
+} yuear_sampling;
+
+/* One named bf16 host tensor, names as in the reference checkpoint
+ * (ar.cpp:216-233): model.embed_tokens.weight, model.norm.weight,
+ * lm_head.weight, model.layers.{i}.{input_layernorm,post_attention_layernorm,
+ * self_attn.{q,k,v,o}_proj,self_attn.{q,k}_norm,mlp.{gate,up,down}_proj}.weight */
+typedef struct yuear_tensor {
+  const char *name;
+  const uint16_t *data;
+  int64_t numel;
+} yuear_tensor;
+
+enum { YUEAR_WEIGHTS_RANDOM = 0, YUEAR_WEIGHTS_HOST = 1 };
+typedef struct yuear_weight_source {
+  int32_t kind;
+  /* RANDOM: linear/embedding weights N(0, std); norm gains 1 + N(0, norm_std) */
+  uint64_t seed;
+  float std, norm_std;
+  /* HOST: every tensor of the model exactly once */
+  const yuear_tensor *tensors;
+  int32_t count;
+} yuear_weight_source;
+
+typedef struct yuear_engine yuear_engine;
+typedef struct yuear_session yuear_session;
+
+/* Per-token callback (types.hpp:27 TokenCallback): phase and native id.
+ * Runs synchronously on the calling thread; must not re-enter. */
+typedef void (*yuear_token_callback)(void *user_data, const char *phase, int32_t token);
+
+/* Borrowed build identity (lyra.h:29). */
+const char *yuear_build_identifier(void);
+void yuear_string_free(char *s); /* lyra.h:54 */
+
+/* ---- engine (replaces ARModel construction, ar.cpp:133-245) ---- */
+yuear_status yuear_engine_create(const yuear_model_config *config,
+                                 const yuear_weight_source *weights,
+                                 yuear_engine **out, char **error_json);
+void yuear_engine_destroy(yuear_engine *engine);
+/* Thread-safe cooperative cancellation of the running call (lyra.h:40). */
+void yuear_engine_cancel(yuear_engine *engine);
+/* Deterministic weight generator (host): the bytes RANDOM sources upload. */
+int32_t yuear_tensor_id(const char *name);
+void yuear_random_tensor(uint64_t seed, int32_t tensor_id, float mean, float std,
+                         int64_t numel, uint16_t *out);
+
+/* ---- generate_tokens (sampling.cpp:185-288, ar.hpp:43-48) ----
+ * phase: "full" (identity map, no end token), "abc" or "semantic".
+ * tokens_out receives up to sampling->max_tokens native ids; *n_out the
+ * count, *truncated 1 when no end token was drawn; *timing_json the timing
+ * keys of sampling.cpp:274-284. Draws use the shared Philox uniforms
+ * u(seed, step, index). */
+yuear_status yuear_generate_tokens(
+    yuear_engine *engine, const int32_t *prefix, int32_t n_prefix,
+    const yuear_sampling *sampling, uint64_t seed, const char *phase,
+    const int32_t *negative, int32_t n_negative, double cfg_scale,
+    int32_t legacy_off, yuear_token_callback on_token, void *user_data,
+    int32_t *tokens_out, int32_t *n_out, int32_t *truncated,
+    char **timing_json, char **error_json);
+
+/* ---- decode-step session (GraphAR, cuda_graph.py:43-240; KVCache,
+ * ar.cpp:98-132) ----
+ * branches in [1, 8] (1 request, 2 = CFG pair, up to 8 independent
+ * sequences); capacity in [1, min(24576, max_position_embeddings)]. */
+yuear_status yuear_session_begin(yuear_engine *engine, int32_t branches,
+                                 int32_t capacity, const char *phase,
+                                 yuear_session **out, char **error_json);
+void yuear_session_end(yuear_session *session);
+/* Appends n ids to one branch (chunked causal prefill, sampling.cpp:152-183);
+ * logits_out (nullable) receives that branch's last-token logits. Fails
+ * without mutation when the capacity would be exceeded (ar.cpp:109-112). */
+yuear_status yuear_session_prefill(yuear_session *session, int32_t branch,
+                                   const int32_t *ids, int32_t n,
+                                   uint16_t *logits_out, char **error_json);
+/* One decode step for every branch (tokens[branches]); captured as one
+ * hipGraph on first use. logits_out (nullable) is [branches][phase size]. */
+yuear_status yuear_session_step(yuear_session *session, const int32_t *tokens,
+                                uint16_t *logits_out, char **error_json);
+/* Runs the device sampler once on the current logits of the session:
+ * CFG merge (cfg_scale != 1 with 2 branches), distribution() with the given
+ * step and history (native ids), then the draw. */
+yuear_status yuear_session_sample(yuear_session *session,
+                                  const yuear_sampling *sampling, uint64_t seed,
+                                  double cfg_scale, int32_t legacy_off,
+                                  int32_t step, const int32_t *history,
+                                  int32_t history_len, int32_t *token_out,
+                                  char **error_json);
+int32_t yuear_session_position(const yuear_session *session, int32_t branch);
+int32_t yuear_session_phase_size(const yuear_session *session);
+/* Cache access for tests/tools: copies slots [0, n) of one layer/branch
+ * (k, v: [Hkv][n][D] bf16). write sets the branch position to n. */
+yuear_status yuear_session_write_kv(yuear_session *session, int32_t layer,
+                                    int32_t branch, const uint16_t *k,
+                                    const uint16_t *v, int32_t n,
+                                    char **error_json);
+yuear_status yuear_session_read_kv(yuear_session *session, int32_t layer,
+                                   int32_t branch, uint16_t *k, uint16_t *v,
+                                   int32_t n, char **error_json);
+/* Test hooks: overwrite the session logits ([branches][phase size]) that the
+ * next yuear_session_sample reads; set one branch's position (the next
+ * slot; stale slots beyond it stay invisible, ar.cpp:124-126). */
+yuear_status yuear_session_write_logits(yuear_session *session,
+                                        const uint16_t *logits, char **error_json);
+yuear_status yuear_session_set_position(yuear_session *session, int32_t branch,
+                                        int32_t position, char **error_json);
+/* One decoder layer decode step (ar.cpp:265-298) on explicit hidden rows
+ * x_in [branches][H], appending at each branch's position (advanced by 1). */
+yuear_status yuear_session_layer_step(yuear_session *session, int32_t layer,
+                                      const uint16_t *x_in, uint16_t *x_out,
+                                      char **error_json);
+/* Mean device time of the last `yuear_session_time_steps` call, and a timed
+ * loop of `steps` graph replays (no host sync between replays) with hipEvents
+ * recorded on the session stream; returns milliseconds per step. */
+yuear_status yuear_session_time_steps(yuear_session *session, int32_t steps,
+                                      double *ms_per_step, char **error_json);
+
+/* Timed device-side greedy/sampled decode loop for benchmarks: `steps`
+ * graph replays of (sampler -> decode step) with no host synchronisation in
+ * between, timed with hipEvents on the session stream. The sampler state
+ * (step counter, history) restarts when reset != 0. tokens_out (nullable)
+ * receives the emitted native ids of this call. */
+yuear_status yuear_session_time_generate(yuear_session *session,
+                                         const yuear_sampling *sampling,
+                                         uint64_t seed, int32_t steps,
+                                         int32_t reset, double *ms_per_step,
+                                         int32_t *tokens_out, char **error_json);
+/* Average device time of one kernel of the decode step, launched `launches`
+ * times back to back on the session stream (GEMVs cycle through the layers
+ * so weights stream from HBM). kernel: "qkv", "attention", "o_proj",
+ * "gate_up", "down", "lm_head" or "sampler". */
+yuear_status yuear_session_time_kernel(yuear_session *session,
+                                       const char *kernel, int32_t launches,
+                                       double *ms_per_launch, char **error_json);
+
+/* ---- op-level entry points (model_ops, ar.hpp:8-19), device pointers,
+ * `stream` is a hipStream_t (NULL = default stream) ---- */
+/* y[b][r] = bf16(x[b] . W[row(r)]) with optional RMSNorm prologue
+ * (norm_w != NULL) and epilogue 0 store / 1 residual add / 2 SwiGLU pairs. */
+int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,
+                      int32_t batch, const uint16_t *dev_x, int32_t x_stride,
+                      const uint16_t *dev_norm_w, float eps, uint16_t *dev_y,
+                      int32_t y_stride, int32_t epilogue, void *stream);
+/* Fused decode attention of one layer (see yuear_session_begin layout):
+ * qkv [batch][(Hq+2Hkv)*128], caches [batch][Hkv][cap][128], pos [batch],
+ * rope tables [positions][64], out [batch][Hq*128]. */
+int32_t yuear_op_attention_decode(
+    const uint16_t *dev_qkv, const uint16_t *dev_q_norm,
+    const uint16_t *dev_k_norm, float eps, const uint16_t *dev_rope_cos,
+    const uint16_t *dev_rope_sin, uint16_t *dev_k_cache, uint16_t *dev_v_cache,
+    const int32_t *dev_pos, int32_t heads, int32_t kv_heads, int32_t capacity,
+    int32_t batch, int32_t max_splits, uint16_t *dev_out, void *stream);
+/* C[m][n] = bf16(A[m] . W[n]) (+ C when residual) on MFMA. */
+int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
+                      int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
+                      int32_t ldc, int32_t residual, void *stream);
+/* Causal fp32-opmath attention for T queries at positions pos0 + t. */
+int32_t yuear_op_attention_prefill(const uint16_t *dev_q,
+                                   const uint16_t *dev_k_cache,
+                                   const uint16_t *dev_v_cache, int32_t tokens,
+                                   int32_t pos0, int32_t heads,
+                                   int32_t kv_heads, int32_t capacity,
+                                   uint16_t *dev_out, void *stream);
+/* RoPE cos/sin tables exactly as the engine builds them (host). */
+void yuear_rope_table(int32_t positions, int32_t head_dim, double theta,
+                      uint16_t *cos_out, uint16_t *sin_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* YUEAR_H */

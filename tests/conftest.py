@@ -1,0 +1,60 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for sub in ("yue2-mlx_amd", "oracle", os.path.join("tests", "golden")):
+    path = os.path.join(ROOT, sub)
+    if path not in sys.path:
+        sys.path.insert(0, path)
+
+# A tiny model of the BASELINE layer family (head_dim 128, GQA 2:1) used by
+# the fast parity tests; the golden fixture tiny_model.npz uses the same one.
+TINY = dict(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=128, vocab_size=512, max_position_embeddings=64,
+            rms_norm_eps=1e-5, rope_theta=500000.0, qk_norm=True)
+
+# The BASELINE 3B decoder (hidden 3072, 24/8 heads, FFN 8192, 28 layers,
+# vocab 83968, eps 1e-5, theta 5e5).
+BASE_3B = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
+               num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=83968,
+               max_position_embeddings=24576, rms_norm_eps=1e-5, rope_theta=500000.0,
+               qk_norm=True)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an AMD Instinct GPU (gfx950) through HIP")
+
+
+def pytest_collection_modifyitems(config, items):
+    gpu_items = [i for i in items if "gpu" in i.keywords]
+    if not gpu_items:
+        return
+    import torch  # imported only when GPU tests are collected
+
+    if not torch.cuda.is_available():
+        skip = pytest.mark.skip(reason="no HIP device in this environment")
+        for item in gpu_items:
+            item.add_marker(skip)
+
+
+def ulps_bf16(a_bits, b_bits):
+    """Distance in bf16 units of the last place between two bf16 arrays."""
+    def ordered(x):
+        x = np.asarray(x, dtype=np.uint16).astype(np.int32)
+        return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + x)
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    import cpu_ref
+    return cpu_ref
+
+
+@pytest.fixture(scope="session")
+def yuear_lib():
+    import yuear
+    return yuear

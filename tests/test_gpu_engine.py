@@ -1,0 +1,261 @@
+"""Engine / session / generate_tokens on the GPU vs the oracle and the golden
+vectors (tiny model of the BASELINE layer family, one BASELINE-shaped layer).
+
+Reference behaviour restated: vendor/yue/tests/test_cuda_graph.py:38-115
+(decode-step equations, cache poisoning, branch isolation, lifecycle,
+capacity validation), tests/test_cache.py (append/overflow), and the
+fidelity methodology of tools/fidelity.py:124-148 (max_abs, argmax).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, TINY, ulps_bf16
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+ATOL, RTOL = 2e-2, 1e-2  # north star logits tolerance (bf16, fp32 accumulate)
+
+
+def f(b):
+    import cpu_ref
+    return cpu_ref.bf16_to_f32(b)
+
+
+def bf(x):
+    import cpu_ref
+    return cpu_ref.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def within(a, b, atol=ATOL, rtol=RTOL):
+    return np.abs(f(a) - f(b)) <= atol + rtol * np.abs(f(b))
+
+
+@pytest.fixture(scope="module")
+def tiny(yuear_lib, oracle):
+    g = np.load(os.path.join(GOLDEN, "tiny_model.npz"))
+    w = yuear_lib.random_weights(TINY, int(g["seed"]), float(g["std"]), float(g["norm_std"]))
+    return yuear_lib.Engine(TINY, w), oracle.Model(TINY, w), g
+
+
+def test_tiny_prefill_and_steps_match_oracle_and_golden(tiny):
+    engine, model, g = tiny
+    s = engine.session(1, 16)
+    cache = model.cache(16)
+    got = [s.prefill(0, g["prefix"].tolist())]
+    want = [model.prefill(g["prefix"].tolist(), cache)]
+    for t in g["steps"]:
+        got.append(s.step(int(t))[0])
+        want.append(model.step(int(t), cache))
+    got, want = np.stack(got), np.stack(want)
+    assert within(got, want).all()
+    assert within(got, g["logits_bf16"]).all()
+    assert (f(got).argmax(1) == f(g["logits_bf16"]).argmax(1)).all()
+    assert ulps_bf16(got, want).max() <= 4
+    assert s.position(0) == len(g["prefix"]) + len(g["steps"])
+
+
+def test_chunked_prefill_is_bit_identical_to_one_pass(tiny):
+    engine, _, _ = tiny
+    ids = [5, 9, 14, 200, 33, 1, 511, 256, 3]
+    a = engine.session(1, 32)
+    full = a.prefill(0, ids)
+    b = engine.session(1, 32)
+    b.prefill(0, ids[:4])
+    part = b.prefill(0, ids[4:])
+    np.testing.assert_array_equal(full, part)
+    for layer in range(TINY["num_hidden_layers"]):
+        ka, va = a.read_kv(layer, 0, len(ids))
+        kb, vb = b.read_kv(layer, 0, len(ids))
+        np.testing.assert_array_equal(ka, kb)
+        np.testing.assert_array_equal(va, vb)
+
+
+def test_decode_step_agrees_with_prefill_path(tiny):
+    engine, _, _ = tiny
+    ids = [7, 8, 9, 10, 11, 12]
+    a = engine.session(1, 16)
+    via_prefill = a.prefill(0, ids)
+    b = engine.session(1, 16)
+    b.prefill(0, ids[:-1])
+    via_step = b.step(ids[-1])[0]
+    assert within(via_step, via_prefill).all()
+
+
+def test_cache_poisoning_and_branch_isolation(tiny):
+    # test_cuda_graph.py:62-79
+    engine, _, _ = tiny
+    prefixes = [[2, 3, 4, 5], [6]]
+    sessions = []
+    for _ in range(2):
+        s = engine.session(2, 12)
+        for b, p in enumerate(prefixes):
+            s.prefill(b, p)
+        sessions.append(s)
+    base, changed = sessions
+    for layer in range(TINY["num_hidden_layers"]):
+        for b, p in enumerate(prefixes):
+            k, v = changed.read_kv(layer, b, 12)
+            k[:, len(p):] = bf(1000.0)
+            v[:, len(p):] = bf(-1000.0)
+            changed.write_kv(layer, b, k, v)
+            changed.set_position(b, len(p))
+    np.testing.assert_array_equal(changed.step(7), base.step(7))
+    for layer in range(TINY["num_hidden_layers"]):  # perturb branch 0's visible cache
+        k, v = changed.read_kv(layer, 0, 5)
+        v[:, :2] = bf(f(v[:, :2]) + 1)
+        changed.write_kv(layer, 0, k, v)
+    old, new = base.step(8), changed.step(8)
+    np.testing.assert_array_equal(new[1], old[1])
+    assert not np.array_equal(new[0], old[0])
+
+
+def test_lifecycle_and_capacity_errors(tiny):
+    engine, _, _ = tiny
+    s = engine.session(1, 5)
+    s.prefill(0, [1, 2, 3])
+    with pytest.raises(ValueError, match="capacity"):
+        s.prefill(0, [4, 5, 6])
+    assert s.position(0) == 3
+    s.step(4)
+    s.step(5)
+    with pytest.raises(ValueError, match="budget"):
+        s.step(6)
+    with pytest.raises(ValueError):
+        s.step(TINY["vocab_size"])
+    with pytest.raises(ValueError):
+        engine.session(1, 0)
+    with pytest.raises(ValueError):
+        engine.session(9, 8)
+    s.close()
+    with pytest.raises(RuntimeError, match="closed"):
+        s.step(1)
+
+
+def test_generate_tokens_greedy_matches_oracle_teacher_forced(tiny, oracle):
+    engine, model, _ = tiny
+    prefix = [3, 17, 255, 1, 98]
+    sampling = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=24)
+    seen = []
+    tokens, timing, truncated = engine.generate_tokens(
+        prefix, sampling, 7, on_token=lambda phase, t: seen.append((phase, t)))
+    assert len(tokens) == 24 and truncated and seen == [("full", t) for t in tokens]
+    assert timing["output_tokens"] == 24 and timing["cfg_branches"] == 1
+    assert set(timing) >= {"seconds", "prefill_seconds", "ttft_seconds", "output_tps",
+                           "prefix_tokens", "execution", "attention", "backend"}
+    cache = model.cache(len(prefix) + 24)
+    logits = model.prefill(prefix, cache)
+    s = oracle.sampling_struct(**sampling)
+    for step, token in enumerate(tokens):
+        scores = oracle.distribution(logits, s, tokens[:step], step, "full")
+        want = oracle.draw(scores, 0.0, 7, step)
+        if want != token:  # only a near-tie may differ (gap-aware accounting)
+            top = np.sort(scores)[-2:]
+            assert top[1] - top[0] <= 2 * (ATOL + RTOL * abs(top[1])), (step, token, want)
+        logits = model.step(token, cache)
+
+
+def test_generate_tokens_cfg_sampled_matches_oracle(tiny, oracle):
+    engine, model, _ = tiny
+    prefix, negative = [3, 17, 255, 1, 98, 400], [9, 8, 7]
+    sampling = dict(temperature=1.0, top_p=0.93, top_k=50, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=20)
+    tokens, timing, _ = engine.generate_tokens(prefix, sampling, 1234, negative=negative,
+                                               cfg_scale=1.5)
+    assert timing["cfg_branches"] == 2 and len(tokens) == 20
+    cp, cn = model.cache(40), model.cache(40)
+    lp, ln = model.prefill(prefix, cp), model.prefill(negative, cn)
+    s = oracle.sampling_struct(**sampling)
+    agree = 0
+    for step, token in enumerate(tokens):
+        scores = oracle.distribution(oracle.guided_logits(lp, ln, 1.5), s, tokens[:step], step,
+                                     "full")
+        agree += oracle.draw(scores, 1.0, 1234, step) == token
+        lp, ln = model.step(token, cp), model.step(token, cn)
+    assert agree >= len(tokens) - 1
+
+
+def test_generate_tokens_validation(tiny):
+    engine, _, _ = tiny
+    ok = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0, penalty_window=50,
+              min_tokens=0, max_tokens=4)
+    with pytest.raises(ValueError, match="negative"):
+        engine.generate_tokens([1, 2], ok, 1, cfg_scale=1.5)
+    with pytest.raises(ValueError, match="24576"):
+        engine.generate_tokens([1] * 10, dict(ok, max_tokens=24570), 1)
+    with pytest.raises(ValueError):
+        engine.generate_tokens([], ok, 1)
+    with pytest.raises(ValueError):
+        engine.generate_tokens([1], dict(ok, top_p=0.0), 1)
+    with pytest.raises(ValueError, match="seed"):
+        engine.generate_tokens([1], ok, 2**63)
+    with pytest.raises(ValueError, match="phase"):
+        engine.generate_tokens([1], ok, 1, phase="lyrics")
+
+
+def test_throwing_callback_cancels(tiny):
+    engine, _, _ = tiny
+    sampling = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=30)
+    calls = []
+
+    def boom(phase, token):
+        calls.append(token)
+        if len(calls) == 3:
+            raise KeyError("stop")
+
+    with pytest.raises(KeyError):
+        engine.generate_tokens([1, 2, 3], sampling, 3, on_token=boom)
+    assert len(calls) == 3
+    tokens, _, _ = engine.generate_tokens([1, 2, 3], sampling, 3)  # engine still usable
+    assert len(tokens) == 30
+
+
+def test_end_token_and_min_tokens_in_semantic_phase(yuear_lib):
+    # Zero layers' weights make the final hidden state the normalised
+    # embedding (all ones), so logits are the row sums of lm_head: only the
+    # end row (MUSIC_END) is positive. Greedy decoding must emit content until
+    # min_tokens and then stop on the end token (sampling.cpp:47-50, 256-259).
+    cfg = dict(hidden_size=64, intermediate_size=64, num_hidden_layers=1,
+               num_attention_heads=1, num_key_value_heads=1, head_dim=128,
+               vocab_size=184704, max_position_embeddings=256, rms_norm_eps=1e-5,
+               rope_theta=1e6)
+    w = {k: np.zeros(s, np.uint16) for k, s in yuear_lib.tensor_shapes(cfg).items()}
+    w["model.embed_tokens.weight"][:] = 0x3F80
+    for k in w:
+        if k.endswith("norm.weight") or "layernorm" in k:
+            w[k][:] = 0x3F80
+    w["lm_head.weight"][151852] = bf(0.01)
+    engine = yuear_lib.Engine(cfg, w)
+    sampling = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.2,
+                    penalty_window=50, min_tokens=5, max_tokens=40)
+    tokens, timing, truncated = engine.generate_tokens([151851, 151853], sampling, 1,
+                                                       phase="semantic")
+    assert tokens == [151853] * 5 and not truncated
+    assert timing["output_tokens"] == 6 and timing["content_tokens"] == 5
+
+
+def test_baseline_layer_step_matches_oracle_and_golden(yuear_lib, oracle):
+    # config 1: one 3072-wide layer, KV N(0,1) over 511 slots, input N(0,1)
+    from make_golden import LAYER
+    g = np.load(os.path.join(GOLDEN, "layer_3072.npz"))
+    seed, length = int(g["seed"]), int(g["length"])
+    w = yuear_lib.random_weights(LAYER, seed)
+    kv = yuear_lib.random_normal(seed, int(g["kv_stream"]), (2, 8, length - 1, 128))
+    x = yuear_lib.random_normal(seed, int(g["x_stream"]), (1, 3072))
+    engine = yuear_lib.Engine(LAYER, w)
+    s = engine.session(1, length)
+    s.write_kv(0, 0, kv[0], kv[1])
+    got = s.layer_step(0, x)[0]
+    model = oracle.Model(LAYER, w)
+    cache = model.cache(length)
+    cache.keys(0)[:, :length - 1] = kv[0]
+    cache.values(0)[:, :length - 1] = kv[1]
+    cache.offset = length - 1
+    want = model.layer(0, x, cache)[0]
+    assert within(got, want).all()
+    assert within(got, g["hidden_bf16"]).all()
+    assert ulps_bf16(got, want).max() <= 4
+    assert s.position(0) == length

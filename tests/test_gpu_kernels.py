@@ -1,0 +1,206 @@
+"""HIP kernels vs the oracle through the C ABI (op-level entry points).
+
+Device memory comes from torch (plumbing only); every computation under test
+runs in libyuear's gfx950 kernels. Tolerances: bf16 results of fp32
+accumulations may differ from the oracle's by the last place when the two
+accumulation orders round differently; stated per test in bf16 ULPs.
+"""
+import numpy as np
+import pytest
+
+from conftest import ulps_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    t.cuda.init()
+    return t
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host(torch, t):
+    torch.cuda.synchronize()
+    out = t.cpu().numpy()
+    return out.view(np.uint16) if out.dtype == np.int16 else out
+
+
+def bf(x):
+    import cpu_ref
+    return cpu_ref.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def f(b):
+    import cpu_ref
+    return cpu_ref.bf16_to_f32(b)
+
+
+GEMV_CASES = [  # (n, k, batch, norm, epilogue)
+    (5120, 3072, 1, True, 0),     # fused QKV + input RMSNorm
+    (3072, 3072, 1, False, 1),    # o_proj + residual
+    (16384, 3072, 1, True, 2),    # gate/up interleaved + SwiGLU
+    (3072, 8192, 1, False, 1),    # down + residual
+    (83968, 3072, 1, True, 0),    # lm_head + final norm
+    (5120, 3072, 2, True, 0),     # CFG pair
+    (3072, 8192, 2, False, 1),
+    (16384, 3072, 2, True, 2),
+    (1024, 3072, 8, True, 0),     # batched sequences
+    (1024, 8192, 8, False, 1),
+    (1000, 256, 3, True, 0),      # ragged: odd batch, short rows, n % 8 != 0
+    (96, 512, 1, False, 2),
+]
+
+
+@pytest.mark.parametrize("n,k,batch,norm,epilogue", GEMV_CASES)
+def test_gemv_matches_oracle(torch, yuear_lib, oracle, n, k, batch, norm, epilogue):
+    rng = np.random.default_rng(n + k + batch)
+    w = bf(rng.normal(size=(n, k)) * 0.02)
+    x = bf(rng.normal(size=(batch, k)))
+    g = bf(1 + rng.normal(size=k) * 0.1)
+    out_n = n // 2 if epilogue == 2 else n
+    y0 = bf(rng.normal(size=(batch, out_n)))
+    h = oracle.rms_norm(x, g, 1e-5) if norm else x
+    acc = oracle.linear(h, w)
+    if epilogue == 0:
+        ref = acc
+    elif epilogue == 1:
+        ref = bf(f(y0) + f(acc))
+    else:
+        ref = oracle.silu_mul(acc[:, 0::2], acc[:, 1::2])
+    dw, dx, dg = dev(torch, w), dev(torch, x), dev(torch, g)
+    dy = dev(torch, y0 if epilogue == 1 else np.zeros((batch, out_n), np.uint16))
+    rc = yuear_lib.lib.yuear_op_gemv(dw.data_ptr(), n, k, batch, dx.data_ptr(), k,
+                                     dg.data_ptr() if norm else None, 1e-5, dy.data_ptr(), out_n,
+                                     epilogue, None)
+    assert rc == 0
+    got = host(torch, dy)
+    d = ulps_bf16(got, ref)
+    assert d.max() <= (3 if epilogue == 2 else 2), d.max()
+    assert (d == 0).mean() > 0.9
+
+
+def prep_qk(oracle, raw, gain, pos, theta=5e5):
+    """q/k RMSNorm over each head, then RoPE at `pos` (ar.cpp:268-277)."""
+    x = oracle.rms_norm(raw, gain, 1e-5) if gain is not None else raw
+    return oracle.rope(x.reshape(1, -1, 128), pos, theta)[0]
+
+
+@pytest.mark.parametrize("heads,kv_heads,batch_pos,splits", [
+    (24, 8, [0], 64), (24, 8, [1], 64), (24, 8, [15], 64), (24, 8, [16], 64),
+    (24, 8, [63], 64), (24, 8, [200], 64), (24, 8, [511], 64), (24, 8, [4095], 64),
+    (24, 8, [4095], 1), (24, 8, [777], 7), (16, 8, [300], 32), (4, 2, [50], 8),
+    (24, 8, [513, 1535], 32), (24, 8, [100, 1200, 7, 2047, 64, 500, 9, 1000], 32),
+])
+def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_heads, batch_pos,
+                                         splits):
+    rng = np.random.default_rng(sum(batch_pos) + heads + splits)
+    B = len(batch_pos)
+    cap = max(batch_pos) + 9
+    qkvw = (heads + 2 * kv_heads) * 128
+    qkv = bf(rng.normal(size=(B, qkvw)))
+    cache_k = bf(rng.normal(size=(B, kv_heads, cap, 128)))
+    cache_v = bf(rng.normal(size=(B, kv_heads, cap, 128)))
+    qn, kn = bf(1 + 0.1 * rng.normal(size=128)), bf(1 + 0.1 * rng.normal(size=128))
+    cos, sin = yuear_lib.rope_table(cap + 1, 128, 5e5)
+    refs, kref, vref = [], [], []
+    for b, pos in enumerate(batch_pos):
+        q = prep_qk(oracle, qkv[b, :heads * 128].reshape(heads, 128), qn, pos)
+        k = prep_qk(oracle, qkv[b, heads * 128:(heads + kv_heads) * 128].reshape(kv_heads, 128),
+                    kn, pos)
+        v = qkv[b, (heads + kv_heads) * 128:].reshape(kv_heads, 128)
+        K, V = cache_k[b].copy(), cache_v[b].copy()
+        K[:, pos], V[:, pos] = k, v
+        refs.append(oracle.attention(q[None], K, V, pos)[0])
+        kref.append(k)
+        vref.append(v)
+    args = [dev(torch, a) for a in (qkv, qn, kn, cos, sin, cache_k, cache_v)]
+    dpos = dev(torch, np.array(batch_pos, np.int32))
+    out = dev(torch, np.zeros((B, heads * 128), np.uint16))
+    rc = yuear_lib.lib.yuear_op_attention_decode(
+        args[0].data_ptr(), args[1].data_ptr(), args[2].data_ptr(), 1e-5, args[3].data_ptr(),
+        args[4].data_ptr(), args[5].data_ptr(), args[6].data_ptr(), dpos.data_ptr(), heads,
+        kv_heads, cap, B, splits, out.data_ptr(), None)
+    assert rc == 0
+    got = host(torch, out)
+    ref = np.stack(refs)
+    d = ulps_bf16(got, ref)
+    assert d.max() <= 3, d.max()
+    assert (d <= 1).mean() > 0.98
+    gk, gv = host(torch, args[5]), host(torch, args[6])
+    for b, pos in enumerate(batch_pos):
+        np.testing.assert_array_equal(gv[b][:, pos], vref[b])
+        assert ulps_bf16(gk[b][:, pos], kref[b]).max() <= 1
+        others = np.ones(cap, bool)
+        others[pos] = False
+        np.testing.assert_array_equal(gk[b][:, others], cache_k[b][:, others])
+
+
+def test_attention_decode_ignores_unused_slots(torch, yuear_lib):
+    # vendor test_cuda_graph.py:62-79: slots beyond the position are invisible
+    rng = np.random.default_rng(9)
+    heads, kv, pos, cap = 24, 8, 300, 400
+    qkv = bf(rng.normal(size=(1, (heads + 2 * kv) * 128)))
+    k = bf(rng.normal(size=(1, kv, cap, 128)))
+    v = bf(rng.normal(size=(1, kv, cap, 128)))
+    cos, sin = yuear_lib.rope_table(cap, 128, 5e5)
+    outs = []
+    for poison in (False, True):
+        kk, vv = k.copy(), v.copy()
+        if poison:
+            kk[..., pos + 1:, :] = bf(1000.0)
+            vv[..., pos + 1:, :] = bf(-1000.0)
+        a = [dev(torch, t) for t in (qkv, cos, sin, kk, vv)]
+        dpos = dev(torch, np.array([pos], np.int32))
+        out = dev(torch, np.zeros((1, heads * 128), np.uint16))
+        assert yuear_lib.lib.yuear_op_attention_decode(
+            a[0].data_ptr(), None, None, 1e-5, a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(),
+            a[4].data_ptr(), dpos.data_ptr(), heads, kv, cap, 1, 16, out.data_ptr(), None) == 0
+        outs.append(host(torch, out))
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("m,n,k,residual", [
+    (1, 256, 256, 0), (7, 1024, 3072, 0), (128, 5120, 3072, 0), (129, 3072, 3072, 1),
+    (300, 1024, 8192, 1), (1000, 384, 512, 0),
+])
+def test_gemm_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual):
+    rng = np.random.default_rng(m * 7 + n)
+    a = bf(rng.normal(size=(m, k)))
+    w = bf(rng.normal(size=(n, k)) * 0.02)
+    c0 = bf(rng.normal(size=(m, n)))
+    acc = oracle.linear(a, w)
+    ref = bf(f(c0) + f(acc)) if residual else acc
+    da, dw = dev(torch, a), dev(torch, w)
+    dc = dev(torch, c0 if residual else np.zeros((m, n), np.uint16))
+    assert yuear_lib.lib.yuear_op_gemm(da.data_ptr(), k, dw.data_ptr(), m, n, k, dc.data_ptr(),
+                                       n, residual, None) == 0
+    d = ulps_bf16(host(torch, dc), ref)
+    assert d.max() <= 2, d.max()
+    assert (d == 0).mean() > 0.9
+
+
+@pytest.mark.parametrize("T,pos0,heads,kv_heads", [(7, 0, 4, 2), (64, 0, 24, 8),
+                                                   (65, 10, 24, 8), (200, 333, 16, 8)])
+def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, heads, kv_heads):
+    rng = np.random.default_rng(T + pos0)
+    cap = pos0 + T + 3
+    q = bf(rng.normal(size=(T, heads, 128)))
+    kc = bf(rng.normal(size=(kv_heads, cap, 128)))
+    vc = bf(rng.normal(size=(kv_heads, cap, 128)))
+    ref = oracle.attention(q, kc, vc, pos0)
+    a = [dev(torch, t) for t in (q, kc, vc)]
+    out = dev(torch, np.zeros((T, heads * 128), np.uint16))
+    assert yuear_lib.lib.yuear_op_attention_prefill(a[0].data_ptr(), a[1].data_ptr(),
+                                                    a[2].data_ptr(), T, pos0, heads, kv_heads,
+                                                    cap, out.data_ptr(), None) == 0
+    d = ulps_bf16(host(torch, out), ref)
+    assert d.max() <= 3, d.max()
+    assert (d <= 1).mean() > 0.98

@@ -1,0 +1,148 @@
+"""Device sampler vs the oracle: identical tokens on identical logits.
+
+The sampler (CFG merge, distribution(), draw) is integer/ordering logic plus
+fp32 arithmetic whose every step is defined on both sides with the same
+operations (portable exp/log, sequential sums in sorted order, Philox
+uniforms), so the drawn token must be bit-identical to the oracle's
+(north star: "a bit-exact sampled token stream when both sides are fed
+identical uniform draws").
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+MUSIC_END, CODEC_OFFSET = 151852, 151853
+
+
+def bf(x):
+    import cpu_ref
+    return cpu_ref.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def head_engine(yuear, vocab):
+    cfg = dict(hidden_size=64, intermediate_size=64, num_hidden_layers=1, num_attention_heads=1,
+               num_key_value_heads=1, head_dim=128, vocab_size=vocab,
+               max_position_embeddings=4096, rms_norm_eps=1e-5, rope_theta=5e5)
+    return yuear.Engine(cfg, seed=1)
+
+
+@pytest.fixture(scope="module")
+def engine_83968(yuear_lib):
+    return head_engine(yuear_lib, 83968)
+
+
+@pytest.fixture(scope="module")
+def engine_yue2(yuear_lib):
+    return head_engine(yuear_lib, 184704)
+
+
+def oracle_token(oracle, logits, sampling, seed, step, history, phase, cfg=1.0, legacy=False):
+    x = logits[0] if cfg == 1.0 else oracle.guided_logits(logits[0], logits[1], cfg)
+    s = oracle.sampling_struct(**sampling)
+    scores = oracle.distribution(x, s, history, step, phase, legacy)
+    local = oracle.draw(scores, sampling["temperature"], seed, step)
+    return oracle.lib().oracle_local_to_native(local, oracle.PHASES[phase])
+
+
+def logits_for(rng, kind, branches, n):
+    if kind == "normal":
+        x = rng.normal(size=(branches, n)) * 2.5
+    elif kind == "ties":  # heavy ties at the top-k / nucleus cut
+        x = np.round(rng.normal(size=(branches, n)) * 2) / 2
+    elif kind == "peaked":
+        x = rng.normal(size=(branches, n))
+        x[:, rng.integers(0, n, 3)] += 12
+    else:  # flat: top-p needs many survivors
+        x = rng.normal(size=(branches, n)) * 0.05
+    return bf(x)
+
+
+CASES = [
+    # name, sampling overrides, branches/cfg, phase, logits kind
+    ("greedy", dict(temperature=0, top_k=1, top_p=1), 1, 1.0, "full", "normal"),
+    ("greedy-ties", dict(temperature=0, top_k=1, top_p=1), 1, 1.0, "full", "ties"),
+    ("cfg3", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "normal"),
+    ("cfg3-ties", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "ties"),
+    ("topk-only", dict(temperature=0.7, top_k=20, top_p=1.0), 1, 1.0, "full", "normal"),
+    ("topp-flat", dict(temperature=1.0, top_k=5000, top_p=0.5), 1, 1.0, "full", "flat"),
+    ("all-vocab", dict(temperature=1.3, top_k=100000, top_p=1.0), 1, 1.0, "full", "normal"),
+    ("peaked", dict(temperature=1.0, top_k=100, top_p=0.95), 1, 1.0, "full", "peaked"),
+]
+
+
+@pytest.mark.parametrize("name,over,branches,cfg,phase,kind", CASES, ids=[c[0] for c in CASES])
+def test_sampler_bit_exact_vs_oracle(engine_83968, oracle, name, over, branches, cfg, phase,
+                                     kind):
+    rng = np.random.default_rng(len(name) * 977)
+    sampling = dict(temperature=1.0, top_p=0.95, top_k=100, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=9000)
+    sampling.update(over)
+    session = engine_83968.session(branches, 64, phase)
+    for trial in range(12):
+        logits = logits_for(rng, kind, branches, 83968)
+        session.write_logits(logits)
+        seed, step = int(rng.integers(0, 2**62)), int(rng.integers(0, 5000))
+        got = session.sample(sampling, seed, step, cfg_scale=cfg)
+        want = oracle_token(oracle, logits, sampling, seed, step, [], phase, cfg)
+        assert got == want, (name, trial, got, want)
+    session.close()
+
+
+def test_sampler_penalty_and_min_tokens_semantic(engine_yue2, oracle):
+    rng = np.random.default_rng(5)
+    sampling = dict(temperature=1.0, top_p=0.95, top_k=100, repetition_penalty=1.2,
+                    penalty_window=50, min_tokens=200, max_tokens=9000)  # semantic defaults
+    session = engine_yue2.session(1, 64, "semantic")
+    n = session.vocab
+    assert n == 32769
+    for trial in range(16):
+        x = rng.normal(size=(1, n)) * 2
+        hist = [CODEC_OFFSET + int(t) for t in rng.integers(0, 40, size=int(rng.integers(0, 90)))]
+        x[0, [h - MUSIC_END for h in hist[-10:]]] += 3  # make the penalty matter
+        x[0, 0] += 6 * (trial % 2)                       # end row high on odd trials
+        logits = bf(x)
+        session.write_logits(logits)
+        step = len(hist) + (0 if trial % 4 < 2 else 300)  # before / after min_tokens
+        seed = int(rng.integers(0, 2**62))
+        got = session.sample(sampling, seed, step, history=hist)
+        want = oracle_token(oracle, logits, sampling, seed, step, hist, "semantic")
+        assert got == want, (trial, got, want)
+    session.close()
+
+
+def test_sampler_legacy_off_bf16_mode(engine_yue2, oracle):
+    rng = np.random.default_rng(6)
+    sampling = dict(temperature=1.0, top_p=0.9, top_k=30, repetition_penalty=1.005,
+                    penalty_window=100, min_tokens=0, max_tokens=4096)
+    session = engine_yue2.session(1, 64, "semantic")
+    for trial in range(8):
+        logits = bf(rng.normal(size=(1, session.vocab)) * 2)
+        session.write_logits(logits)
+        hist = [CODEC_OFFSET + int(t) for t in rng.integers(0, 50, size=30)]
+        seed = int(rng.integers(0, 2**62))
+        got = session.sample(sampling, seed, 31, history=hist, legacy_off=True)
+        want = oracle_token(oracle, logits, sampling, seed, 31, hist, "semantic", legacy=True)
+        assert got == want, (trial, got, want)
+    session.close()
+
+
+def test_sampler_known_answers_on_device(engine_yue2):
+    # test_sampling.py:37-49 restated through the device sampler: only the
+    # surviving rows can ever be drawn.
+    session = engine_yue2.session(1, 64, "semantic")
+    n = session.vocab
+    base = np.full((1, n), -20.0, np.float32)
+    base[0, 1:5] = [5, 4, 4, 3]
+    session.write_logits(bf(base))
+    drawn = {session.sample(dict(temperature=1.0, top_k=2, top_p=1.0, repetition_penalty=1.0,
+                                 min_tokens=0, max_tokens=100), seed, 0) - MUSIC_END
+             for seed in range(200)}
+    assert drawn == {1, 2, 3}
+    base[0, 1:5] = [5, 4, 3, 2]
+    session.write_logits(bf(base))
+    drawn = {session.sample(dict(temperature=1.0, top_k=4, top_p=0.01, repetition_penalty=1.0,
+                                 min_tokens=0, max_tokens=100), seed, 0) - MUSIC_END
+             for seed in range(50)}
+    assert drawn == {1}
+    session.close()

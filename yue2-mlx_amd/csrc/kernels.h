@@ -1,0 +1,130 @@
+// Kernel parameter blocks and host launchers for the gfx950 AR decode path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yuear {
+
+enum GemvEpilogue : int {
+  kEpiStore = 0,     // y = bf16(acc)
+  kEpiResidual = 1,  // y = bf16(y + bf16(acc))                 (ar.cpp:292-298)
+  kEpiSwiGLU = 2,    // rows (2i, 2i+1) = (gate_i, up_i):
+                     // y[i] = bf16(bf16(silu(bf16(g))) * bf16(u)) (ar.cpp:36-51)
+};
+
+// y[b, r] = x[b, :] . W[row(r), :], bf16 in, fp32 accumulate.
+struct GemvParams {
+  const uint16_t *w = nullptr;  // [rows][k]
+  int n = 0;                    // output rows (phase-local rows for lm_head)
+  int k = 0;
+  int batch = 1;
+  const uint16_t *x = nullptr;  // [batch][x_stride]
+  int x_stride = 0;
+  const uint16_t *embed = nullptr;  // optional gather table [vocab][k]
+  const int32_t *tokens = nullptr;  // [batch] rows of `embed`
+  int embed_rows = 0;               // token ids are clamped to [0, embed_rows)
+  uint16_t *x_out = nullptr;        // gathered rows are stored here (block 0)
+  const uint16_t *norm_w = nullptr; // optional RMSNorm prologue gain [k]
+  float eps = 1e-6f;
+  uint16_t *y = nullptr;
+  int y_stride = 0;
+  int epilogue = kEpiStore;
+  int seg0_start = 0, seg0_len = 1 << 30, seg1_start = 0;  // row map
+  int32_t *advance = nullptr;  // block 0 increments advance[0..batch)
+};
+hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
+
+// Split-K flash-decode attention for one layer, all branches, with the
+// q/k RMSNorm + RoPE prologue, the KV append of the current token and the
+// last-block merge of the split partials fused in.
+struct AttnDecodeParams {
+  const uint16_t *qkv = nullptr;  // [batch][qkv_stride] raw projections
+  int qkv_stride = 0;
+  const uint16_t *q_norm = nullptr, *k_norm = nullptr;  // [D] or null
+  float eps = 1e-6f;
+  const uint16_t *rope_cos = nullptr, *rope_sin = nullptr;  // [positions][D/2]
+  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [batch][Hkv][cap][D]
+  const int32_t *pos = nullptr;  // [batch] slot of the current token
+  int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0, batch = 1;
+  int max_splits = 1;
+  float *part_o = nullptr;   // [batch][Hkv][max_splits][G][D]
+  float *part_ml = nullptr;  // [batch][Hkv][max_splits][G][2]
+  int32_t *counters = nullptr;  // [batch][Hkv], zero between launches
+  uint16_t *out = nullptr;      // [batch][out_stride]
+  int out_stride = 0;
+};
+hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s);
+
+// Device sampler: CFG merge + distribution() + draw, one token per call.
+struct SamplerParams {
+  const uint16_t *logits = nullptr;  // [branches][n] phase-local bf16
+  int n = 0;
+  int branches = 1;
+  float cfg_scale = 1.0f;  // applied when branches == 2 and != 1
+  float temperature = 0.f, top_p = 1.f;
+  int top_k = 1;
+  int min_tokens = 0;
+  int penalty_window = 0;
+  const float *alphas = nullptr;  // [window+1] pow(penalty, count), or null
+  int phase = kPhaseFull;
+  int vocab = 0;
+  uint64_t seed = 0;
+  int legacy_off = 0;
+  int32_t *state = nullptr;   // [0]=step counter, [1]=done flag
+  int32_t *history = nullptr; // [max_tokens] native tokens emitted so far
+  int hist_len = -1;          // history length; < 0: the step counter
+  int max_tokens = 0;         // appends history[step] while step < max_tokens
+  int32_t *tokens_out = nullptr;  // [branches] next input token (native)
+  float *scratch = nullptr;       // [n] fp32 scores
+  uint32_t *scratch_u = nullptr;  // [2 * n] survivor keys / indices
+};
+hipError_t launch_sampler(const SamplerParams &p, hipStream_t s);
+
+// ---- prefill ----
+struct GemmParams {
+  const uint16_t *a = nullptr;  // [m][k] activations
+  int lda = 0;
+  const uint16_t *w = nullptr;  // [n][k] weights
+  int m = 0, n = 0, k = 0;
+  uint16_t *c = nullptr;        // [m][ldc]
+  int ldc = 0;
+  int residual = 0;             // c = bf16(c + bf16(acc))
+};
+hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
+
+hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
+                             int width, uint16_t *out, hipStream_t s);
+hipError_t launch_rms_norm_rows(const uint16_t *x, int rows, int width,
+                                const uint16_t *w, float eps, uint16_t *y,
+                                hipStream_t s);
+hipError_t launch_swiglu_rows(const uint16_t *gu, int rows, int f, uint16_t *out,
+                              hipStream_t s);
+
+// q/k RMSNorm + RoPE for T tokens at absolute positions pos0 + t; writes q
+// [T][Hq][D] and appends K/V at slots pos0 + t of one branch's cache.
+struct QkPrepParams {
+  const uint16_t *qkv = nullptr;  // [T][qkv_stride]
+  int qkv_stride = 0;
+  int tokens = 0;
+  const uint16_t *q_norm = nullptr, *k_norm = nullptr;
+  float eps = 1e-6f;
+  const uint16_t *rope_cos = nullptr, *rope_sin = nullptr;
+  int pos0 = 0;
+  int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0;
+  uint16_t *q_out = nullptr;  // [T][Hq][D]
+  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // this branch [Hkv][cap][D]
+};
+hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s);
+
+// Causal attention for T queries at positions pos0 + t over keys [0, pos0+t]
+// with fp32 opmath (ar.cpp:284-291). out [T][Hq*D].
+struct AttnPrefillParams {
+  const uint16_t *q = nullptr;  // [T][Hq][D]
+  const uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [Hkv][cap][D]
+  int tokens = 0, pos0 = 0;
+  int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0;
+  uint16_t *out = nullptr;
+};
+hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s);
+
+}  // namespace yuear
