@@ -77,6 +77,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-launches", type=int, default=112)
+    ap.add_argument("--kernel-only", default=None,
+                    help="profiling mode: only time this decode kernel (e.g. gate_up)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="profiling mode: one device-to-device copy of MIB MiB (counter scale)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -86,6 +90,17 @@ def main():
     import numpy as np
     import torch
     import yuear
+
+    if args.copy_calibration:
+        # HBM counter calibration: a plain copy of known size (read N, write N)
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n}), flush=True)
+        return
 
     t_start = time.perf_counter()
     c = CONFIG
@@ -98,6 +113,12 @@ def main():
     capacity = prefill + W + K + 8
     session = engine.session(1, capacity)
     rng = np.random.default_rng(args.seed)
+    if args.kernel_only:
+        session.prefill(0, rng.integers(0, c["vocab_size"], size=64).tolist())
+        ms = session.time_kernel(args.kernel_only, args.kernel_launches)
+        print(json.dumps({"kernel": args.kernel_only, "launches": args.kernel_launches,
+                          "us": ms * 1e3}), flush=True)
+        return
     prompt = rng.integers(0, c["vocab_size"], size=prefill).tolist()
     t = time.perf_counter()
     session.prefill(0, prompt)

@@ -43,8 +43,24 @@ inline uint16_t f2bf(float f) {
 }
 inline float rbf(float f) { return bf2f(f2bf(f)); }
 
+// Accumulation mode of the dot products: 0 = fp32 in a fixed blocked order
+// (the default), 1 = fp64 (a more accurate restatement, used to measure how
+// far two valid fp32 accumulation orders can drift apart over many layers).
+int g_accumulate = 0;
+
 // fp32 dot product in a fixed blocked order (16 partial sums, pairwise).
 float dot_f32_bf16(const float *x, const uint16_t *w, int k) {
+  if (g_accumulate == 1) {
+    double acc[8] = {0};
+    int i = 0;
+    for (; i + 8 <= k; i += 8)
+      for (int j = 0; j < 8; ++j)
+        acc[j] += double(x[i + j]) * double(bf2f(w[i + j]));
+    double s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    for (; i < k; ++i)
+      s += double(x[i]) * double(bf2f(w[i]));
+    return float(s);
+  }
   float acc[16] = {0};
   int i = 0;
   for (; i + 16 <= k; i += 16)
@@ -104,6 +120,8 @@ extern "C" {
 
 uint16_t oracle_f2bf(float x) { return f2bf(x); }
 float oracle_bf2f(uint16_t x) { return bf2f(x); }
+
+void oracle_set_accumulation(int mode) { g_accumulate = mode; }
 
 void oracle_set_threads(int n) {
 #ifdef _OPENMP

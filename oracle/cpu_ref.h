@@ -76,6 +76,8 @@ float oracle_uniform(uint64_t seed, int32_t step, int32_t index);
 float oracle_plog(float x);
 float oracle_pexp(float x);
 void oracle_set_threads(int n);
+/* 0: fp32 blocked accumulation (default); 1: fp64 accumulation. */
+void oracle_set_accumulation(int mode);
 
 /* ---- model_ops (ar.cpp:19-96) ---- */
 void oracle_rms_norm(const uint16_t *x, int rows, int n, const uint16_t *w,

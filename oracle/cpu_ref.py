@@ -58,6 +58,7 @@ def _load():
         "oracle_plog": (C.c_float, [C.c_float]),
         "oracle_pexp": (C.c_float, [C.c_float]),
         "oracle_set_threads": (None, [C.c_int]),
+        "oracle_set_accumulation": (None, [C.c_int]),
         "oracle_rms_norm": (None, [u16p, C.c_int, C.c_int, u16p, C.c_float, u16p]),
         "oracle_linear": (None, [u16p, C.c_int, C.c_int, u16p, C.c_int, u16p]),
         "oracle_rope": (None, [u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double]),

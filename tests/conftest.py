@@ -48,6 +48,23 @@ def ulps_bf16(a_bits, b_bits):
     return np.abs(ordered(a_bits) - ordered(b_bits))
 
 
+def assert_close_bf16(got_bits, ref_bits, rtol=2.0 ** -7, atol_frac=2.0 ** -9, scale=None,
+                      exact_frac=0.8):
+    """|got - ref| <= rtol |ref| + atol_frac * scale (scale: max |ref| unless
+    given), and at least `exact_frac` of the elements bit-identical. bf16
+    results of fp32 work that rounds differently sit within one unit of the
+    last place of the operands' scale, which near zero is many ULPs of the
+    result, so ULP counts are not used as the bound."""
+    import cpu_ref
+    g, r = cpu_ref.bf16_to_f32(got_bits), cpu_ref.bf16_to_f32(ref_bits)
+    s = np.abs(r).max() if scale is None else scale
+    err = np.abs(g - r)
+    bound = rtol * np.abs(r) + atol_frac * s
+    assert (err <= bound).all(), f"max err {err.max():.3g}, worst ratio {(err / bound).max():.3g}"
+    same = np.mean(np.asarray(got_bits) == np.asarray(ref_bits))
+    assert same >= exact_frac, f"only {same:.3f} bit-identical"
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import cpu_ref

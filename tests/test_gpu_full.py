@@ -1,24 +1,47 @@
 """The BASELINE 3B decoder at full size on the GPU vs the oracle.
 
 28 layers, hidden 3072, 24/8 heads, FFN 8192, vocab 83968, N(0, 0.02)
-weights with unit norm gains (the bench's model). The oracle's CPU decode step
-is ~1 s at this size, so these tests compare a few teacher-forced steps:
-after a short prefill, and at KV length 4096 (the benchmark's metric point)
-with the GPU's own cache copied to the oracle so both sides decode the same
-state.
+weights with unit norm gains (the bench's model).
+
+Tolerance. Over 28 bf16 layers two valid implementations drift apart by far
+more than one rounding: the oracle run with fp32 accumulation and the same
+oracle run with fp64 accumulation already differ by ~0.1 in max |logit|
+(scale ~5). Full-size parity therefore follows the reference's own fidelity
+rule (tools/limits.py:21-79, tools/fidelity.py:124-148): the GPU's distance to
+the higher-precision anchor (oracle, fp64 accumulation) must stay within
+twice the distance of the bf16/fp32 oracle to that anchor, in max_abs and in
+rms, with the cosine and the argmax checked too. The strict 2e-2/1e-2 logit
+tolerance is asserted where it holds (tiny model, single BASELINE layer:
+test_gpu_engine.py).
 """
 import numpy as np
 import pytest
 
-from conftest import BASE_3B, ulps_bf16
+from conftest import BASE_3B
 
 pytestmark = pytest.mark.gpu
-ATOL, RTOL = 2e-2, 1e-2
 
 
 def f(b):
     import cpu_ref
-    return cpu_ref.bf16_to_f32(b)
+    return cpu_ref.bf16_to_f32(b).astype(np.float64)
+
+
+def metrics(a, b):
+    d = f(a) - f(b)
+    cos = np.dot(f(a), f(b)) / (np.linalg.norm(f(a)) * np.linalg.norm(f(b)))
+    return {"max_abs": np.abs(d).max(), "rms": np.sqrt(np.mean(d * d)), "cos": cos}
+
+
+def check_fidelity(gpu, oracle32, oracle64):
+    radius = metrics(oracle32, oracle64)
+    got = metrics(gpu, oracle64)
+    print("oracle radius", radius, "gpu", got)
+    assert got["max_abs"] <= 2 * radius["max_abs"]
+    assert got["rms"] <= 2 * radius["rms"]
+    assert 1 - got["cos"] <= 2 * (1 - radius["cos"])
+    top = np.sort(f(oracle64))[-2:]
+    assert f(gpu).argmax() == f(oracle64).argmax() or top[1] - top[0] < 2 * radius["max_abs"]
 
 
 @pytest.fixture(scope="module")
@@ -26,44 +49,57 @@ def pair(yuear_lib, oracle):
     w = yuear_lib.random_weights(BASE_3B, 20251201)
     engine = yuear_lib.Engine(BASE_3B, w)
     model = oracle.Model(BASE_3B, w)
-    yield engine, model
+    yield engine, model, oracle
+    oracle.lib().oracle_set_accumulation(0)
     engine.close()
 
 
-def check_logits(got, want):
-    d = np.abs(f(got) - f(want))
-    assert (d <= ATOL + RTOL * np.abs(f(want))).all(), d.max()
-    assert f(got).argmax() == f(want).argmax() or \
-        np.sort(f(want))[-1] - np.sort(f(want))[-2] < 2 * ATOL
-    return ulps_bf16(got, want)
+def oracle_run(oracle, mode, fn):
+    oracle.lib().oracle_set_accumulation(mode)
+    try:
+        return fn()
+    finally:
+        oracle.lib().oracle_set_accumulation(0)
 
 
 def test_full_model_short_prefill_and_steps(pair):
-    engine, model = pair
+    engine, model, oracle = pair
     rng = np.random.default_rng(1)
-    prefix = rng.integers(0, 83968, size=24).tolist()
-    s = engine.session(1, 64)
-    cache = model.cache(64)
-    check_logits(s.prefill(0, prefix), model.prefill(prefix, cache))
-    for t in rng.integers(0, 83968, size=2).tolist():
-        check_logits(s.step(t)[0], model.step(t, cache))
+    prefix = rng.integers(0, 83968, size=12).tolist()
+    steps = rng.integers(0, 83968, size=2).tolist()
+    s = engine.session(1, 32)
+    gpu = [s.prefill(0, prefix)] + [s.step(t)[0] for t in steps]
     s.close()
+    ref = {}
+    for mode in (0, 1):
+        def run():
+            cache = model.cache(32)
+            return [model.prefill(prefix, cache)] + [model.step(t, cache) for t in steps]
+        ref[mode] = oracle_run(oracle, mode, run)
+    for g, r32, r64 in zip(gpu, ref[0], ref[1]):
+        check_fidelity(g, r32, r64)
 
 
 def test_full_model_decode_at_kv_4096(pair):
-    engine, model = pair
+    engine, model, oracle = pair
     rng = np.random.default_rng(2)
     prefix = rng.integers(0, 83968, size=4095).tolist()
     s = engine.session(1, 4100)
     s.prefill(0, prefix)
-    cache = model.cache(4100)
-    for layer in range(BASE_3B["num_hidden_layers"]):
-        k, v = s.read_kv(layer, 0, 4095)
-        cache.keys(layer)[:, :4095] = k
-        cache.values(layer)[:, :4095] = v
-    cache.offset = 4095
+    kv = [s.read_kv(layer, 0, 4095) for layer in range(BASE_3B["num_hidden_layers"])]
     token = int(rng.integers(0, 83968))
-    check_logits(s.step(token)[0], model.step(token, cache))  # L = 4096
-    k, v = s.read_kv(0, 0, 4096)  # the appended slot equals the oracle's
-    assert ulps_bf16(k[:, 4095], cache.keys(0)[:, 4095]).max() <= 1
+    gpu = s.step(token)[0]  # L = 4096
+    k_new = s.read_kv(0, 0, 4096)[0][:, 4095]
     s.close()
+    ref = {}
+    for mode in (0, 1):
+        cache = model.cache(4100)
+        for layer, (k, v) in enumerate(kv):
+            cache.keys(layer)[:, :4095] = k
+            cache.values(layer)[:, :4095] = v
+        cache.offset = 4095
+        ref[mode] = oracle_run(oracle, mode, lambda: model.step(token, cache))
+        if mode == 0:
+            from conftest import ulps_bf16
+            assert ulps_bf16(k_new, cache.keys(0)[:, 4095]).max() <= 1
+    check_fidelity(gpu, ref[0], ref[1])

@@ -1,14 +1,15 @@
 """HIP kernels vs the oracle through the C ABI (op-level entry points).
 
 Device memory comes from torch (plumbing only); every computation under test
-runs in libyuear's gfx950 kernels. Tolerances: bf16 results of fp32
-accumulations may differ from the oracle's by the last place when the two
-accumulation orders round differently; stated per test in bf16 ULPs.
+runs in libyuear's gfx950 kernels. Tolerances (conftest.assert_close_bf16):
+bf16 results of fp32 accumulations may differ from the oracle's by one unit
+of the last place of the operands' scale when the two accumulation orders
+round differently; most elements must be bit-identical.
 """
 import numpy as np
 import pytest
 
-from conftest import ulps_bf16
+from conftest import assert_close_bf16, ulps_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -82,9 +83,8 @@ def test_gemv_matches_oracle(torch, yuear_lib, oracle, n, k, batch, norm, epilog
                                      epilogue, None)
     assert rc == 0
     got = host(torch, dy)
-    d = ulps_bf16(got, ref)
-    assert d.max() <= (3 if epilogue == 2 else 2), d.max()
-    assert (d == 0).mean() > 0.9
+    scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+    assert_close_bf16(got, ref, scale=scale, exact_frac=0.9)
 
 
 def prep_qk(oracle, raw, gain, pos, theta=5e5):
@@ -131,9 +131,7 @@ def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_hea
     assert rc == 0
     got = host(torch, out)
     ref = np.stack(refs)
-    d = ulps_bf16(got, ref)
-    assert d.max() <= 3, d.max()
-    assert (d <= 1).mean() > 0.98
+    assert_close_bf16(got, ref, exact_frac=0.8)
     gk, gv = host(torch, args[5]), host(torch, args[6])
     for b, pos in enumerate(batch_pos):
         np.testing.assert_array_equal(gv[b][:, pos], vref[b])
@@ -182,9 +180,8 @@ def test_gemm_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual):
     dc = dev(torch, c0 if residual else np.zeros((m, n), np.uint16))
     assert yuear_lib.lib.yuear_op_gemm(da.data_ptr(), k, dw.data_ptr(), m, n, k, dc.data_ptr(),
                                        n, residual, None) == 0
-    d = ulps_bf16(host(torch, dc), ref)
-    assert d.max() <= 2, d.max()
-    assert (d == 0).mean() > 0.9
+    scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+    assert_close_bf16(host(torch, dc), ref, scale=scale, exact_frac=0.9)
 
 
 @pytest.mark.parametrize("T,pos0,heads,kv_heads", [(7, 0, 4, 2), (64, 0, 24, 8),
@@ -201,6 +198,4 @@ def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, hea
     assert yuear_lib.lib.yuear_op_attention_prefill(a[0].data_ptr(), a[1].data_ptr(),
                                                     a[2].data_ptr(), T, pos0, heads, kv_heads,
                                                     cap, out.data_ptr(), None) == 0
-    d = ulps_bf16(host(torch, out), ref)
-    assert d.max() <= 3, d.max()
-    assert (d <= 1).mean() > 0.98
+    assert_close_bf16(host(torch, out), ref, exact_frac=0.8)

@@ -111,6 +111,30 @@ def test_sampler_penalty_and_min_tokens_semantic(engine_yue2, oracle):
     session.close()
 
 
+@pytest.mark.parametrize("branches,cfg", [(1, 1.0), (2, 1.5)])
+def test_greedy_with_penalty_and_end_mask(engine_yue2, oracle, branches, cfg):
+    # the greedy path rescored only the penalised / masked rows: odd phase
+    # size (32769) exercises the padded rows and the scalar tail
+    rng = np.random.default_rng(7 + branches)
+    sampling = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.3,
+                    penalty_window=20, min_tokens=50, max_tokens=9000)
+    session = engine_yue2.session(branches, 64, "semantic")
+    n = session.vocab
+    for trial in range(16):
+        x = rng.normal(size=(branches, n))
+        hist = [CODEC_OFFSET + int(t) for t in rng.integers(0, 30, size=40)]
+        x[:, [h - MUSIC_END for h in hist[-20:]]] += 4      # penalised rows lead
+        x[:, 0] += 5 * (trial % 2)                          # end row leads on odd trials
+        x[:, n - 1] += 3 * (trial % 3 == 0)                 # the tail row
+        logits = bf(x)
+        session.write_logits(logits)
+        step = 10 if trial % 4 < 2 else 60                  # masked / unmasked end row
+        got = session.sample(sampling, 0, step, history=hist, cfg_scale=cfg)
+        want = oracle_token(oracle, logits, sampling, 0, step, hist, "semantic", cfg)
+        assert got == want, (trial, got, want)
+    session.close()
+
+
 def test_sampler_legacy_off_bf16_mode(engine_yue2, oracle):
     rng = np.random.default_rng(6)
     sampling = dict(temperature=1.0, top_p=0.9, top_k=30, repetition_penalty=1.005,

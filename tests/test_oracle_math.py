@@ -238,3 +238,23 @@ def test_baseline_layer_matches_torch_golden(oracle):
     got = f(model.layer(0, x, cache)[0])
     assert close(got, f(g["hidden_bf16"])).all()
     assert close(got, g["hidden_f32"], atol=5e-2).all()
+
+
+def test_fp64_accumulation_mode_is_the_tighter_anchor(oracle):
+    # the anchor used by the full-size fidelity tests: fp64 accumulation must
+    # sit at least as close to the exact result as the default fp32 order
+    rng = np.random.default_rng(8)
+    x = bf(rng.normal(size=(3, 8192)))
+    w = bf(rng.normal(size=(512, 8192)) * 0.02)
+    exact = f(x).astype(np.float64) @ f(w).astype(np.float64).T
+    y32 = f(oracle.linear(x, w))
+    oracle.lib().oracle_set_accumulation(1)
+    try:
+        y64 = f(oracle.linear(x, w))
+    finally:
+        oracle.lib().oracle_set_accumulation(0)
+    e32, e64 = np.abs(y32 - exact), np.abs(y64 - exact)
+    assert e64.sum() <= e32.sum()
+    # fp64 then one rounding: the nearest bf16 (within half a bf16 ulp)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(exact), 1e-30))) - 7)
+    assert (e64 <= 0.5 * ulp * (1 + 1e-6)).all()

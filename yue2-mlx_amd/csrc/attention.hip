@@ -38,12 +38,38 @@ __device__ __forceinline__ void unpack8(u32x4 v, float *f) {
   f[6] = bflo(v.w); f[7] = bfhi(v.w);
 }
 
+constexpr int kMaxSplits = 64;
+
+// s_waitcnt vmcnt(0): this wave's outstanding vector memory operations
+// (including stores) have completed. gfx9 encoding: vmcnt in bits [3:0] and
+// [15:14] (zero here), expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Load coherent at device (agent) scope: served past any stale per-XCD L2 line.
+__device__ __forceinline__ float coherent_load(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void load_tile(const u32x4 *kc, const u32x4 *vc, int t0, int wave,
+                                          int grp, int sub, int last_cached, u32x4 *kr,
+                                          u32x4 *vr) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // keys at or beyond the current slot come from LDS (or are masked); the
+    // clamp keeps every address inside the written part of the cache
+    const int kk = min(t0 + wave * 16 + i * 4 + grp, last_cached);
+    kr[i] = kc[size_t(kk) * (D / 8) + sub];
+    vr[i] = vc[size_t(kk) * (D / 8) + sub];
+  }
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, float scale) {
   __shared__ float q_lds[G][D];        // scaled query (fp32), log2(e) folded in
   __shared__ u32x4 kv_new[2][D / 8];   // current key / value (bf16)
   __shared__ float w_m[4][G], w_l[4][G];
   __shared__ float w_o[4][G][D];
+  __shared__ float s_m[kMaxSplits][G], s_w[kMaxSplits][G], s_den[G];
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -63,7 +89,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
   const size_t part = (size_t(b) * Hkv + kvh) * p.max_splits;
 
   if (active) {
-    // ---- prologue: q heads (waves 0..), current k, current v ----
+    const int grp = lane >> 4, sub = lane & 15;
+    const int last_cached = pos > 0 ? pos - 1 : 0;
+    // first K/V tile in flight before the prologue's dependent work
+    u32x4 kr[4], vr[4];
+    load_tile(kc, vc, s0, wave, grp, sub, last_cached, kr, vr);
+
+    // ---- prologue: q heads, current k, current v ----
     const uint16_t *row = p.qkv + size_t(b) * p.qkv_stride;
     const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
     const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
@@ -95,8 +127,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
       *dst = kv_new[which][c];
     }
 
-    // ---- main loop ----
-    const int grp = lane >> 4, sub = lane & 15;
+    // ---- main loop: 64 keys per pass, next tile prefetched ----
     float q[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -113,19 +144,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
         o_run[h][e] = 0.f;
     }
     for (int t0 = s0; t0 < s1; t0 += 64) {
-      u32x4 kr[4], vr[4];
-      int key[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        key[i] = t0 + wave * 16 + i * 4 + grp;
-        const int kk = min(key[i], pos > 0 ? pos - 1 : 0);
-        kr[i] = kc[size_t(kk) * (D / 8) + sub];
-        vr[i] = vc[size_t(kk) * (D / 8) + sub];
-      }
+      u32x4 kn[4], vn[4];
+      load_tile(kc, vc, t0 + 64, wave, grp, sub, last_cached, kn, vn);
       float sc[4][G];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (key[i] == pos) {
+        const int key = t0 + wave * 16 + i * 4 + grp;
+        if (key == pos) {
           kr[i] = kv_new[0][sub];
           vr[i] = kv_new[1][sub];
         }
@@ -133,15 +158,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
         unpack8(kr[i], kf);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          float a = 0.f;
+          float acc = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            a = fmaf(q[h][e], kf[e], a);
-          a += __shfl_xor(a, 8, 64);
-          a += __shfl_xor(a, 4, 64);
-          a += __shfl_xor(a, 2, 64);
-          a += __shfl_xor(a, 1, 64);
-          sc[i][h] = key[i] < s1 ? a : -__builtin_inff();
+            acc = fmaf(q[h][e], kf[e], acc);
+          acc += __shfl_xor(acc, 8, 64);
+          acc += __shfl_xor(acc, 4, 64);
+          acc += __shfl_xor(acc, 2, 64);
+          acc += __shfl_xor(acc, 1, 64);
+          sc[i][h] = key < s1 ? acc : -__builtin_inff();
         }
       }
 #pragma unroll
@@ -173,6 +198,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
             o_run[h][e] = fmaf(pw[i], vf[e], o_run[h][e]);
         }
         m_run[h] = m_new;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kr[i] = kn[i];
+        vr[i] = vn[i];
       }
     }
     // reduce the four 16-lane groups of the wave
@@ -211,43 +241,89 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
         o = fmaf(f, w_o[w][h][d], o);
         l = fmaf(f, w_l[w][h], l);
       }
-      p.part_o[(part + s) * (G * D) + e] = o;
+      // write-through (agent-scope) stores: visible to every XCD once complete
+      __hip_atomic_store(&p.part_o[(part + s) * (G * D) + e], o, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
-        p.part_ml[((part + s) * G + h) * 2] = M;
-        p.part_ml[((part + s) * G + h) * 2 + 1] = l;
+        __hip_atomic_store(&p.part_ml[((part + s) * G + h) * 2], M, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&p.part_ml[((part + s) * G + h) * 2 + 1], l, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
 
-  // ---- arrival; the last workgroup of this (b, kv head) merges ----
-  __threadfence();
+  // ---- arrival. Every wave waits for its write-through partial stores to
+  // complete (vmcnt(0); a workgroup barrier alone does not wait for memory),
+  // then one counter increment per workgroup. The last workgroup of this
+  // (b, kv head) reads the partials with agent-scope loads and merges. No
+  // cache-wide write-back or invalidate is needed on this path. ----
+  wait_vmem();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&p.counters[b * Hkv + kvh], 1);
+    const int prev = __hip_atomic_fetch_add(&p.counters[b * Hkv + kvh], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == int(gridDim.x) - 1;
   }
   __syncthreads();
   if (!is_last)
     return;
-  __threadfence();
   const int n_active = (L + chunk - 1) / chunk;
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int h = e / D, d = e % D;
+  // One memory round: this thread's partial-o loads (up to kMergeBatch splits
+  // per output) are issued together with the (m, l) staging loads.
+  constexpr int kMergeBatch = 32;
+  constexpr int kOutPerThread = (G * D + 255) / 256;
+  float ov[kOutPerThread][kMergeBatch];
+#pragma unroll
+  for (int r = 0; r < kOutPerThread; ++r) {
+    const int e = min(int(threadIdx.x) + 256 * r, G * D - 1);
+    const float *po = p.part_o + part * (G * D) + e;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j)
+      ov[r][j] = coherent_load(po + size_t(min(j, n_active - 1)) * (G * D));
+  }
+  for (int i = threadIdx.x; i < n_active * G; i += 256) {
+    const int t = i / G, h = i - t * G;
+    s_m[t][h] = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
+    s_w[t][h] = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);  // l, made a weight below
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int h = threadIdx.x;
     float M = -__builtin_inff();
     for (int t = 0; t < n_active; ++t)
-      M = fmaxf(M, p.part_ml[((part + t) * G + h) * 2]);
-    float num = 0.f, den = 0.f;
+      M = fmaxf(M, s_m[t][h]);
+    float den = 0.f;
     for (int t = 0; t < n_active; ++t) {
-      const float m = p.part_ml[((part + t) * G + h) * 2];
-      const float l = p.part_ml[((part + t) * G + h) * 2 + 1];
-      const float f = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - M);
-      num = fmaf(f, p.part_o[(part + t) * (G * D) + e], num);
-      den = fmaf(f, l, den);
+      const float f = s_m[t][h] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(s_m[t][h] - M);
+      s_m[t][h] = f;
+      den = fmaf(f, s_w[t][h], den);
     }
-    p.out[size_t(b) * p.out_stride + size_t(kvh * G + h) * D + d] = f2bf(num / den);
+    s_den[h] = den;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_active * G; i += 256) {
+    const int t = i / G, h = i - t * G;
+    s_w[t][h] = s_m[t][h] / s_den[h];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kOutPerThread; ++r) {
+    const int e = int(threadIdx.x) + 256 * r;
+    if (e >= G * D)
+      break;
+    const int h = e / D;
+    const float *po = p.part_o + part * (G * D) + e;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j)
+      acc = j < n_active ? fmaf(s_w[j][h], ov[r][j], acc) : acc;
+    for (int t = kMergeBatch; t < n_active; ++t)  // more than kMergeBatch splits
+      acc = fmaf(s_w[t][h], coherent_load(po + size_t(t) * (G * D)), acc);
+    p.out[size_t(b) * p.out_stride + size_t(kvh * G) * D + e] = f2bf(acc);
   }
   if (threadIdx.x == 0)
-    atomicExch(&p.counters[b * Hkv + kvh], 0);
+    __hip_atomic_store(&p.counters[b * Hkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int G>
@@ -262,7 +338,7 @@ hipError_t launch_g(const AttnDecodeParams &p, hipStream_t s) {
 
 hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s) {
   if (p.head_dim != D || p.kv_heads < 1 || p.heads % p.kv_heads || p.max_splits < 1 ||
-      p.batch < 1 || p.capacity < 1)
+      p.max_splits > kMaxSplits || p.batch < 1 || p.capacity < 1)
     return hipErrorInvalidValue;
   switch (p.heads / p.kv_heads) {
   case 1: return launch_g<1>(p, s);

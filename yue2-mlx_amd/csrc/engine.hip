@@ -230,6 +230,7 @@ struct LayerW {
 
 struct PhaseInfo {
   int kind, size, end, seg0_start, seg0_len, seg1_start;
+  int stride() const { return (size + 7) & ~7; }  // logits row stride (16-byte rows)
 };
 PhaseInfo phase_info(const std::string &name, int vocab) {
   if (name == "full")
@@ -517,9 +518,15 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.qkv = S.alloc<uint16_t>(size_t(branches) * c.qkv());
   S.attn = S.alloc<uint16_t>(size_t(branches) * c.Hq * c.D);
   S.act = S.alloc<uint16_t>(size_t(branches) * c.F);
-  S.logits = S.alloc<uint16_t>(size_t(branches) * S.phase.size);
-  // split-K: about two workgroups per CU at batch 1 for long contexts
-  S.max_splits = std::max(1, std::min(64, (capacity + 63) / 64));
+  S.logits = S.alloc<uint16_t>(size_t(branches) * S.phase.stride());
+  // split-K: up to 64 splits of >= 128 keys (256 workgroups at KV 4096,
+  // batch 1, 8 kv heads); YUEAR_ATTN_KEYS_PER_SPLIT overrides the target
+  {
+    int keys = 128;
+    if (const char *env = std::getenv("YUEAR_ATTN_KEYS_PER_SPLIT"))
+      keys = std::max(16, std::atoi(env));
+    S.max_splits = std::max(1, std::min(64, (capacity + keys - 1) / keys));
+  }
   const int G = c.Hq / c.Hkv;
   S.part_o = S.alloc<float>(size_t(branches) * c.Hkv * S.max_splits * G * c.D);
   S.part_ml = S.alloc<float>(size_t(branches) * c.Hkv * S.max_splits * G * 2);
@@ -546,7 +553,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.host_pos.assign(branches, 0);
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_tok), size_t(kContext + 16) * 4));
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_logits),
-                     size_t(branches) * S.phase.size * 2));
+                     size_t(branches) * S.phase.stride() * 2));
   HIPC(hipStreamSynchronize(S.stream));
 }
 
@@ -661,7 +668,7 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   h.norm_w = E.final_norm;
   h.eps = c.eps;
   h.y = out;
-  h.y_stride = S.phase.size;
+  h.y_stride = S.phase.stride();
   h.seg0_start = S.phase.seg0_start;
   h.seg0_len = S.phase.seg0_len;
   h.seg1_start = S.phase.seg1_start;
@@ -804,13 +811,13 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
     }
     S.host_pos[b] += T;
     if (start + T >= n)  // final norm + projection of the last hidden row
-      enqueue_head(S, S.px + size_t(T - 1) * c.H, 1, c.H, S.logits + size_t(b) * S.phase.size,
-                   nullptr);
+      enqueue_head(S, S.px + size_t(T - 1) * c.H, 1, c.H,
+                   S.logits + size_t(b) * S.phase.stride(), nullptr);
     HIPC(hipStreamSynchronize(st));
   }
   set_device_pos(S);
   if (logits_out) {
-    HIPC(hipMemcpyAsync(S.pin_logits, S.logits + size_t(b) * S.phase.size,
+    HIPC(hipMemcpyAsync(S.pin_logits, S.logits + size_t(b) * S.phase.stride(),
                         size_t(S.phase.size) * 2, hipMemcpyDeviceToHost, st));
     HIPC(hipStreamSynchronize(st));
     std::memcpy(logits_out, S.pin_logits, size_t(S.phase.size) * 2);
@@ -834,10 +841,12 @@ void step(yuear_session &S, const int32_t *tokens, uint16_t *logits_out) {
   for (int b = 0; b < S.B; ++b)
     S.host_pos[b] += 1;
   if (logits_out) {
-    const size_t bytes = size_t(S.B) * S.phase.size * 2;
-    HIPC(hipMemcpyAsync(S.pin_logits, S.logits, bytes, hipMemcpyDeviceToHost, S.stream));
+    const size_t ls = S.phase.stride(), n = S.phase.size;
+    HIPC(hipMemcpyAsync(S.pin_logits, S.logits, size_t(S.B) * ls * 2, hipMemcpyDeviceToHost,
+                        S.stream));
     HIPC(hipStreamSynchronize(S.stream));
-    std::memcpy(logits_out, S.pin_logits, bytes);
+    for (int b = 0; b < S.B; ++b)
+      std::memcpy(logits_out + b * n, S.pin_logits + b * ls, n * 2);
   } else {
     HIPC(hipStreamSynchronize(S.stream));
   }
@@ -848,6 +857,7 @@ SamplerParams sampler_params(yuear_session &S, const yuear_sampling &s, uint64_t
   SamplerParams p;
   p.logits = S.logits;
   p.n = S.phase.size;
+  p.ls = S.phase.stride();
   p.branches = S.B;
   p.cfg_scale = float(cfg_scale);
   p.temperature = float(s.temperature);
@@ -1050,7 +1060,8 @@ yuear_status yuear_session_write_logits(yuear_session *S, const uint16_t *logits
     if (!S || !logits)
       invalid("session and logits are required");
     HIPC(hipStreamSynchronize(S->stream));
-    HIPC(hipMemcpy(S->logits, logits, size_t(S->B) * S->phase.size * 2, hipMemcpyHostToDevice));
+    HIPC(hipMemcpy2D(S->logits, size_t(S->phase.stride()) * 2, logits, size_t(S->phase.size) * 2,
+                     size_t(S->phase.size) * 2, S->B, hipMemcpyHostToDevice));
   });
 }
 

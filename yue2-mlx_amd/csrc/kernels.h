@@ -57,8 +57,9 @@ hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s);
 
 // Device sampler: CFG merge + distribution() + draw, one token per call.
 struct SamplerParams {
-  const uint16_t *logits = nullptr;  // [branches][n] phase-local bf16
+  const uint16_t *logits = nullptr;  // [branches][ls] phase-local bf16
   int n = 0;
+  int ls = 0;  // logits row stride (multiple of 8 elements)
   int branches = 1;
   float cfg_scale = 1.0f;  // applied when branches == 2 and != 1
   float temperature = 0.f, top_p = 1.f;

@@ -29,14 +29,20 @@ constexpr int kWaves = kT / 64;
 constexpr int kSortLds = 4096;  // survivors sorted in LDS up to this count
 
 struct Shared {
+  union {
+    struct {
+      uint32_t key[kSortLds];
+      uint32_t idx[kSortLds];
+    } sort;
+    uint32_t bits[2 * kSortLds];  // special-index bitmap (up to 262144 rows)
+  } u;
   uint32_t hist[2048];
   int wave_tmp[kWaves];
   float wave_val[kWaves];
   int wave_idx[kWaves];
   int pen_loc[128];
   int bcast[4];
-  uint32_t sort_key[kSortLds];
-  uint32_t sort_idx[kSortLds];
+  int count;
   float prob[kSortLds];
   uint8_t keep[kSortLds];
 };
@@ -86,6 +92,10 @@ __device__ int block_scan(int x, Shared &sh, int *total) {
   return v + before;
 }
 
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
 // Block argmax with the lowest index winning ties; result broadcast.
 __device__ void block_argmax(float val, int idx, Shared &sh, float *out_val, int *out_idx) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -93,7 +103,7 @@ __device__ void block_argmax(float val, int idx, Shared &sh, float *out_val, int
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(val, o, 64);
     const int i2 = __shfl_xor(idx, o, 64);
-    if (v2 > val || (v2 == val && i2 < idx)) {
+    if (better(v2, i2, val, idx)) {
       val = v2;
       idx = i2;
     }
@@ -106,11 +116,9 @@ __device__ void block_argmax(float val, int idx, Shared &sh, float *out_val, int
   float bv = sh.wave_val[0];
   int bi = sh.wave_idx[0];
   for (int w = 1; w < kWaves; ++w) {
-    const float v2 = sh.wave_val[w];
-    const int i2 = sh.wave_idx[w];
-    if (v2 > bv || (v2 == bv && i2 < bi)) {
-      bv = v2;
-      bi = i2;
+    if (better(sh.wave_val[w], sh.wave_idx[w], bv, bi)) {
+      bv = sh.wave_val[w];
+      bi = sh.wave_idx[w];
     }
   }
   __syncthreads();
@@ -141,6 +149,50 @@ __device__ void bitonic(uint32_t *key, uint32_t *idx, int n) {
   }
 }
 
+struct Ctx {
+  const SamplerParams &p;
+  bool legacy, cfg;
+  float ninf;
+  __device__ float cast(float v) const { return legacy ? rbf(v) : v; }
+  // Score of the 8 logits of chunk c (sampling.cpp:44 and the CFG merge of
+  // sampling.cpp:100-115), before penalty and temperature.
+  __device__ void chunk(int c, float *out) const {
+    const u32x4 a = reinterpret_cast<const u32x4 *>(p.logits)[c];
+    const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+    if (!cfg) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        out[2 * q] = bflo(av[q]);
+        out[2 * q + 1] = bfhi(av[q]);
+      }
+      return;
+    }
+    const u32x4 u = reinterpret_cast<const u32x4 *>(p.logits + p.ls)[c];
+    const uint32_t uv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      out[2 * q] = guided(bflo(av[q]), bflo(uv[q]));
+      out[2 * q + 1] = guided(bfhi(av[q]), bfhi(uv[q]));
+    }
+  }
+  __device__ float one(int i) const {
+    if (!cfg) return bf2f(p.logits[i]);
+    return guided(bf2f(p.logits[i]), bf2f(p.logits[p.ls + i]));
+  }
+  __device__ float guided(float c, float u) const {
+    const float delta = rbf(c - u);
+    const float scaled = rbf(delta * p.cfg_scale);
+    return rbf(u + scaled);
+  }
+  __device__ float temp(float v) const {
+    return p.temperature != 0.f && p.temperature != 1.0f ? cast(v / p.temperature) : v;
+  }
+};
+
+__device__ __forceinline__ bool special(const Shared &sh, int i) {
+  return (sh.u.bits[i >> 5] >> (i & 31)) & 1u;
+}
+
 __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
   __shared__ Shared sh;
   const int tid = threadIdx.x;
@@ -149,78 +201,113 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
     return;  // the end token was already drawn
   const int step = p.state[0];
   const bool greedy = p.temperature == 0.f;
-  const bool legacy = p.legacy_off != 0;
-  const float ninf = -__builtin_inff();
+  const Ctx cx{p, p.legacy_off != 0, p.branches == 2 && p.cfg_scale != 1.0f, -__builtin_inff()};
+  const float ninf = cx.ninf;
   const int end = p.phase == kPhaseAbc ? kEOD : p.phase == kPhaseSemantic ? 0 : -1;
-  float *sc = p.scratch;
-  auto cast = [&](float v) { return legacy ? rbf(v) : v; };
+  const bool end_masked = end >= 0 && end < n && step < p.min_tokens;  // sampling.cpp:47-50
 
-  // 1. scores (sampling.cpp:44-50, 100-115)
-  const bool cfg = p.branches == 2 && p.cfg_scale != 1.0f;
-  for (int i = tid; i < n; i += kT) {
-    float s;
-    if (cfg) {
-      const float c = bf2f(p.logits[i]), u = bf2f(p.logits[n + i]);
-      const float delta = rbf(c - u);
-      const float scaled = rbf(delta * p.cfg_scale);
-      s = rbf(u + scaled);
-    } else {
-      s = bf2f(p.logits[i]);
-    }
-    if (i == end && step < p.min_tokens)
-      s = ninf;
-    sc[i] = s;
-  }
-  __syncthreads();
-
-  // 2. windowed repetition penalty (sampling.cpp:51-75)
+  // Special rows: the end row while masked and the distinct local ids of the
+  // penalty window (sampling.cpp:51-75); everything else is a plain score.
+  const int nw = (n + 31) >> 5;
+  for (int i = tid; i < nw; i += kT)
+    sh.u.bits[i] = 0;
   const int hlen = p.hist_len < 0 ? step : p.hist_len;
-  if (p.alphas && p.penalty_window > 0 && hlen > 0) {
-    const int wlen = min(hlen, p.penalty_window);
-    if (tid < wlen)
-      sh.pen_loc[tid] = local_of(p.history[hlen - wlen + tid], p.phase, p.vocab);
-    __syncthreads();
-    if (tid < wlen) {
-      const int loc = sh.pen_loc[tid];
-      bool first = loc >= 0 && loc < n;
-      int count = 0;
-      for (int t = 0; t < wlen; ++t) {
-        if (sh.pen_loc[t] == loc) {
-          ++count;
-          if (t < tid) first = false;
-        }
+  const int wlen = p.alphas && p.penalty_window > 0 ? min(hlen, p.penalty_window) : 0;
+  if (tid < wlen)
+    sh.pen_loc[tid] = local_of(p.history[hlen - wlen + tid], p.phase, p.vocab);
+  __syncthreads();
+  int pen_count = 0;  // > 0: this thread owns a distinct penalised row
+  if (tid < wlen) {
+    const int loc = sh.pen_loc[tid];
+    bool first = loc >= 0 && loc < n;
+    for (int t = 0; t < wlen; ++t)
+      if (sh.pen_loc[t] == loc) {
+        ++pen_count;
+        if (t < tid) first = false;
       }
-      if (first) {
-        const float a = p.alphas[count];
-        const float v = sc[loc];
-        sc[loc] = v < 0.f ? cast(v * a) : cast(v / a);
-      }
-    }
-    __syncthreads();
+    if (first)
+      atomicOr(&sh.u.bits[loc >> 5], 1u << (loc & 31));
+    else
+      pen_count = 0;
   }
+  if (tid == 0 && end_masked)
+    atomicOr(&sh.u.bits[end >> 5], 1u << (end & 31));
+  __syncthreads();
+  // full score of a special row: mask, then penalty (a masked -inf stays -inf)
+  auto special_score = [&](int loc, int count) {
+    float v = cx.one(loc);
+    if (loc == end && end_masked)
+      v = ninf;
+    if (count > 0) {
+      const float a = p.alphas[count];
+      v = v < 0.f ? cx.cast(v * a) : cx.cast(v / a);
+    }
+    return v;
+  };
 
+  const int n8 = n >> 3;
   int local = 0;
-  if (greedy) {  // 3. argmax (sampling.cpp:247)
+  if (greedy) {  // sampling.cpp:247: argmax, lowest index on ties
     float bv = ninf;
     int bi = 0x7fffffff;
-    for (int i = tid; i < n; i += kT) {
-      const float v = sc[i];
-      if (v > bv || (v == bv && i < bi)) {
-        bv = v;
+    for (int c0 = tid; c0 < n8; c0 += 2 * kT) {
+      float v[2][8];
+      const int c1 = min(c0 + kT, n8 - 1);
+      cx.chunk(c0, v[0]);
+      cx.chunk(c1, v[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 1 && c0 + kT >= n8) break;
+        const int base = 8 * (h ? c1 : c0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (!special(sh, base + e) && better(v[h][e], base + e, bv, bi)) {
+            bv = v[h][e];
+            bi = base + e;
+          }
+      }
+    }
+    for (int i = 8 * n8 + tid; i < n; i += kT)
+      if (!special(sh, i) && better(cx.one(i), i, bv, bi)) {
+        bv = cx.one(i);
         bi = i;
+      }
+    if (pen_count > 0) {
+      const int loc = sh.pen_loc[tid];
+      const float v = special_score(loc, pen_count);
+      if (better(v, loc, bv, bi)) {
+        bv = v;
+        bi = loc;
       }
     }
     float rv;
     block_argmax(bv, bi, sh, &rv, &local);
+    if (local == 0x7fffffff) local = 0;
   } else {
-    // 4a. temperature (sampling.cpp:78-81)
-    if (p.temperature != 1.0f) {
-      for (int i = tid; i < n; i += kT)
-        sc[i] = cast(sc[i] / p.temperature);
-      __syncthreads();
+    float *sc = p.scratch;
+    // 4a. scores with penalty and temperature (sampling.cpp:44-81)
+    for (int c = tid; c < n8; c += kT) {
+      float v[8];
+      cx.chunk(c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        v[e] = cx.temp(v[e]);
+      reinterpret_cast<float4 *>(sc)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4 *>(sc)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
     }
-    // 4b. k-th largest threshold (sampling.cpp:82-84)
+    for (int i = 8 * n8 + tid; i < n; i += kT)
+      sc[i] = cx.temp(cx.one(i));
+    __syncthreads();
+    if (pen_count > 0) {
+      const int loc = sh.pen_loc[tid];
+      sc[loc] = cx.temp(special_score(loc, pen_count));
+    }
+    if (tid == 0 && end_masked)
+      sc[end] = ninf;
+    __syncthreads();
+    // 4b. k-th largest threshold (sampling.cpp:82-84): 3-pass radix select
     const int k = min(p.top_k, n);
+    const int n4 = n >> 2;
     uint32_t thr_key = 0;
     if (k < n) {
       uint32_t prefix = 0, pmask = 0;
@@ -233,7 +320,17 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
         for (int i = tid; i < 2048; i += kT)
           sh.hist[i] = 0;
         __syncthreads();
-        for (int i = tid; i < n; i += kT) {
+        for (int c = tid; c < n4; c += kT) {
+          const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+          const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t key = order_key(fv[e]);
+            if ((key & pmask) == prefix)
+              atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+          }
+        }
+        for (int i = 4 * n4 + tid; i < n; i += kT) {
           const uint32_t key = order_key(sc[i]);
           if ((key & pmask) == prefix)
             atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
@@ -259,22 +356,24 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
       }
       thr_key = prefix;
     }
-    // 4c. ordered compaction of survivors (score >= threshold)
-    const int per = (n + kT - 1) / kT;
-    const int lo = min(n, tid * per), hi = min(n, lo + per);
-    int cnt = 0;
-    for (int i = lo; i < hi; ++i)
-      cnt += order_key(sc[i]) >= thr_key;
-    int n_s;
-    const int incl = block_scan(cnt, sh, &n_s);
-    uint32_t *surv = p.scratch_u;  // [n] survivor indices, index order
-    {
-      int o = incl - cnt;
-      for (int i = lo; i < hi; ++i)
-        if (order_key(sc[i]) >= thr_key)
-          surv[o++] = uint32_t(i);
-    }
+    // 4c. survivors (score >= threshold, ties kept), compacted in any order:
+    // the nucleus sort and the draw's index tie-break restore determinism
+    if (tid == 0) sh.count = 0;
     __syncthreads();
+    uint32_t *surv = p.scratch_u;  // [n] survivor indices
+    for (int c = tid; c < n4; c += kT) {
+      const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+      const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (order_key(fv[e]) >= thr_key)
+          surv[atomicAdd(&sh.count, 1)] = uint32_t(4 * c + e);
+    }
+    for (int i = 4 * n4 + tid; i < n; i += kT)
+      if (order_key(sc[i]) >= thr_key)
+        surv[atomicAdd(&sh.count, 1)] = uint32_t(i);
+    __syncthreads();
+    const int n_s = sh.count;
 
     float bv = ninf;
     int bi = 0x7fffffff;
@@ -285,7 +384,7 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
         const float v = sc[i];
         if (!(v > ninf)) continue;
         const float key = v + gumbel(draw_uniform(p.seed, step, i));
-        if (key > bv || (key == bv && i < bi)) {
+        if (better(key, i, bv, bi)) {
           bv = key;
           bi = i;
         }
@@ -295,8 +394,9 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
       int P = 1;
       while (P < n_s) P <<= 1;
       const bool in_lds = P <= kSortLds;
-      uint32_t *key = in_lds ? sh.sort_key : p.scratch_u + n;
-      uint32_t *idx = in_lds ? sh.sort_idx : p.scratch_u + n + P;
+      uint32_t *key = in_lds ? sh.u.sort.key : p.scratch_u + n;
+      uint32_t *idx = in_lds ? sh.u.sort.idx : p.scratch_u + n + P;
+      __syncthreads();  // the bitmap shares storage with the LDS sort arrays
       for (int r = tid; r < P; r += kT) {
         if (r < n_s) {
           const int i = int(surv[r]);
@@ -319,12 +419,12 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
         float total = 0.f;  // sequential sum in sorted order
         for (int r = 0; r < n_s; ++r)
           total += prob[r];
-        const int minimum = legacy ? 3 : 1;
+        const int minimum = cx.legacy ? 3 : 1;
         float cum = 0.f;
         for (int r = 0; r < n_s; ++r) {
-          const float pr = legacy ? rbf(prob[r] / total) : prob[r] / total;
-          cum = cast(cum + pr);
-          const float pre = cast(cum - pr);
+          const float pr = cx.legacy ? rbf(prob[r] / total) : prob[r] / total;
+          cum = cx.cast(cum + pr);
+          const float pre = cx.cast(cum - pr);
           const bool removed = pre > p.top_p && r >= minimum;
           if (keep)
             keep[r] = !removed;
@@ -340,7 +440,7 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
         const float v = sc[i];
         if (!(v > ninf)) continue;
         const float gk = v + gumbel(draw_uniform(p.seed, step, i));
-        if (gk > bv || (gk == bv && i < bi)) {
+        if (better(gk, i, bv, bi)) {
           bv = gk;
           bi = i;
         }
@@ -366,8 +466,9 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
 }  // namespace
 
 hipError_t launch_sampler(const SamplerParams &p, hipStream_t s) {
-  if (p.n < 1 || p.branches < 1 || p.branches > 8 || p.penalty_window > 128 || !p.scratch ||
-      !p.scratch_u || !p.state || !p.tokens_out)
+  if (p.n < 1 || p.n > 64 * kSortLds || p.ls < p.n || p.ls % 8 || p.branches < 1 ||
+      p.branches > 8 || p.penalty_window > 128 || !p.scratch || !p.scratch_u || !p.state ||
+      !p.tokens_out)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(sampler_kernel, dim3(1), dim3(kT), 0, s, p);
   return hipGetLastError();
