@@ -83,7 +83,7 @@ struct Phase {
 
 // sampling.cpp:8-18 and ar.cpp:302-323. The FULL phase is this build's
 // identity projection for vocabularies that do not hold the YuE2 protocol rows
-// (the BASELINE-shaped random models); it has no end token.
+// (the 3B-shaped random models); it has no end token.
 bool phase_of(int phase, int vocab, Phase &p) {
   switch (phase) {
   case ORACLE_PHASE_FULL:

@@ -10,15 +10,15 @@ for sub in ("yue2-mlx_amd", "oracle", os.path.join("tests", "golden")):
     if path not in sys.path:
         sys.path.insert(0, path)
 
-# A tiny model of the BASELINE layer family (head_dim 128, GQA 2:1) used by
+# A tiny model of the 3B layer family (head_dim 128, GQA 2:1) used by
 # the fast parity tests; the golden fixture tiny_model.npz uses the same one.
 TINY = dict(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
             num_key_value_heads=2, head_dim=128, vocab_size=512, max_position_embeddings=64,
             rms_norm_eps=1e-5, rope_theta=500000.0, qk_norm=True)
 
-# The BASELINE 3B decoder (hidden 3072, 24/8 heads, FFN 8192, 28 layers,
+# The 3B AR decoder (hidden 3072, 24/8 heads, FFN 8192, 28 layers,
 # vocab 83968, eps 1e-5, theta 5e5).
-BASE_3B = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
+MODEL_3B = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
                num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=83968,
                max_position_embeddings=24576, rms_norm_eps=1e-5, rope_theta=500000.0,
                qk_norm=True)

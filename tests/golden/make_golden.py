@@ -9,7 +9,7 @@ on CPU in bf16 and fp32, and stores only inputs' seeds and outputs:
 
   tiny_model.npz   2-layer model (H 256, F 512, 4/2 heads, D 128, V 512):
                    logits after a 7-token prefill and 3 teacher-forced steps
-  layer_3072.npz   one BASELINE-shaped layer (H 3072, 24/8 heads, F 8192,
+  layer_3072.npz   one 3B-shaped layer (H 3072, 24/8 heads, F 8192,
                    eps 1e-5, theta 5e5), KV cache N(0,1) for 511 slots, input
                    hidden N(0,1), decode at slot 511: output hidden
 

@@ -10,7 +10,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from conftest import BASE_3B, ROOT, TINY
+from conftest import MODEL_3B, ROOT, TINY
 
 HEADER = os.path.join(ROOT, "include", "yuear.h")
 LIB = os.path.join(ROOT, "yue2-mlx_amd", "libyuear.so")
@@ -39,7 +39,7 @@ def test_build_identifier(yuear_lib):
 
 
 def test_tensor_ids_cover_every_reference_name(yuear_lib):
-    shapes = yuear_lib.tensor_shapes(BASE_3B)
+    shapes = yuear_lib.tensor_shapes(MODEL_3B)
     ids = [yuear_lib.lib.yuear_tensor_id(n.encode()) for n in shapes]
     assert min(ids) >= 0 and len(set(ids)) == len(ids) == 3 + 28 * 11
     for bad in (b"model.layers.x.mlp.up_proj.weight", b"lm_head", b"model.layers.0.mlp.weight"):

@@ -1,0 +1,191 @@
+"""Persistent decode step (one launch per token) against the per-op decode
+kernels on the GPU.
+
+The persistent kernel repeats the per-op kernels' arithmetic operation for
+operation, so the two paths must agree bit for bit: logits of every step,
+every KV slot appended, positions; and through the sampler, the emitted
+tokens. The per-op path itself is pinned against the oracle and the golden
+vectors in test_gpu_engine.py / test_gpu_full.py; this file closes the chain
+for the persistent path (ar.cpp:246-323 decode step, sampling.cpp:185-288
+loop). Shapes cover both compiled hidden sizes, one and two branches, ragged
+branch lengths, a single-split cache, a 33-split cache at KV ~4096 and the
+semantic phase's odd logits row count (32769 rows, a ragged last task).
+"""
+import numpy as np
+import pytest
+
+from conftest import MODEL_3B
+
+pytestmark = pytest.mark.gpu
+
+TWO_LAYER = dict(MODEL_3B, num_hidden_layers=2)
+# the semantic phase reads the native codec rows [151852, 151852 + 32769)
+TWO_LAYER_NATIVE = dict(TWO_LAYER, vocab_size=184704)
+HIDDEN_2048 = dict(hidden_size=2048, intermediate_size=6144, num_hidden_layers=3,
+                   num_attention_heads=16, num_key_value_heads=8, head_dim=128, vocab_size=8192,
+                   max_position_embeddings=4096, rms_norm_eps=1e-6, rope_theta=1e6, qk_norm=True)
+
+
+@pytest.fixture(scope="module")
+def engine(yuear_lib):
+    e = yuear_lib.Engine(TWO_LAYER, None, seed=11)
+    yield e
+    e.close()
+
+
+def run(engine, path, branches, capacity, prompts, steps, phase="full"):
+    print(f"[decode] path={path} branches={branches} cap={capacity} "
+          f"prompts={[len(p) for p in prompts]} steps={len(steps)} phase={phase}", flush=True)
+    s = engine.session(branches, capacity, phase)
+    s.decode_path = path
+    assert s.decode_path == path
+    for b, p in enumerate(prompts):
+        s.prefill(b, p)
+    logits = np.stack([s.step(t) for t in steps])
+    pos = [s.position(b) for b in range(branches)]
+    layers = engine.config["num_hidden_layers"]
+    kv = [s.read_kv(layer, b, pos[b]) for layer in range(layers) for b in range(branches)]
+    s.close()
+    return logits, kv, pos
+
+
+def assert_same(a, b):
+    la, kva, pa = a
+    lb, kvb, pb = b
+    assert pa == pb
+    np.testing.assert_array_equal(la, lb)
+    for (ka, va), (kb, vb) in zip(kva, kvb):
+        np.testing.assert_array_equal(ka, kb)
+        np.testing.assert_array_equal(va, vb)
+
+
+@pytest.mark.parametrize("branches,capacity,lengths,n_steps", [
+    (1, 64, [5], 6),
+    (1, 20, [1], 18),           # one split; fills the cache to its last slot
+    (2, 700, [513, 200], 4),    # ragged branches
+    (1, 4200, [4090], 3),       # 33 splits around KV 4096
+])
+def test_persistent_step_matches_per_op_kernels_bitwise(engine, branches, capacity, lengths,
+                                                        n_steps):
+    rng = np.random.default_rng(capacity + branches)
+    V = engine.config["vocab_size"]
+    prompts = [rng.integers(0, V, size=n).tolist() for n in lengths]
+    steps = [rng.integers(0, V, size=branches).tolist() for _ in range(n_steps)]
+    a = run(engine, "kernels", branches, capacity, prompts, steps)
+    b = run(engine, "persistent", branches, capacity, prompts, steps)
+    assert_same(a, b)
+    assert np.isfinite(a[0].view(np.uint16).astype(np.float32)).all()
+
+
+def test_semantic_phase_odd_row_count(yuear_lib):
+    e = yuear_lib.Engine(TWO_LAYER_NATIVE, None, seed=5)
+    try:
+        rng = np.random.default_rng(3)
+        prompts = [rng.integers(0, 184704, size=40).tolist()]
+        steps = [[int(t)] for t in rng.integers(151853, 151853 + 32768, size=3)]
+        a = run(e, "kernels", 1, 64, prompts, steps, phase="semantic")
+        b = run(e, "persistent", 1, 64, prompts, steps, phase="semantic")
+        assert a[0].shape[-1] == 32769
+        assert_same(a, b)
+    finally:
+        e.close()
+
+
+def test_hidden_2048_two_branches(yuear_lib):
+    e = yuear_lib.Engine(HIDDEN_2048, None, seed=9)
+    try:
+        rng = np.random.default_rng(4)
+        prompts = [rng.integers(0, 8192, size=n).tolist() for n in (100, 37)]
+        steps = [rng.integers(0, 8192, size=2).tolist() for _ in range(5)]
+        assert_same(run(e, "kernels", 2, 300, prompts, steps),
+                    run(e, "persistent", 2, 300, prompts, steps))
+    finally:
+        e.close()
+
+
+def test_unsupported_shape_keeps_per_op_path(yuear_lib):
+    from conftest import TINY
+    e = yuear_lib.Engine(TINY, None, seed=1)
+    try:
+        s = e.session(1, 16)
+        assert s.decode_path == "kernels"
+        with pytest.raises(ValueError, match="persistent decode step is not available"):
+            s.decode_path = "persistent"
+        s.close()
+    finally:
+        e.close()
+
+
+GREEDY = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0, penalty_window=50,
+              min_tokens=0, max_tokens=64)
+SAMPLED = dict(temperature=0.9, top_p=0.9, top_k=40, repetition_penalty=1.1, penalty_window=20,
+               min_tokens=0, max_tokens=64)
+
+
+@pytest.mark.parametrize("sampling", [GREEDY, SAMPLED], ids=["greedy", "sampled"])
+def test_device_loop_tokens_agree(engine, sampling):
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, 83968, size=77).tolist()
+    out = {}
+    for path in ("kernels", "persistent"):
+        s = engine.session(1, 256)
+        s.decode_path = path
+        last = s.prefill(0, prompt)
+        ms, tokens = s.time_generate(sampling, 1234, 24, reset=True)
+        out[path] = (tokens, s.position(0), s.read_kv(1, 0, s.position(0)))
+        s.close()
+        assert ms > 0 and last.shape == (83968,)
+    assert out["kernels"][0] == out["persistent"][0]
+    assert out["kernels"][1] == out["persistent"][1]
+    np.testing.assert_array_equal(out["kernels"][2][0], out["persistent"][2][0])
+
+
+def test_generate_tokens_on_persistent_path(engine, monkeypatch):
+    rng = np.random.default_rng(9)
+    prefix = rng.integers(0, 83968, size=50).tolist()
+    sampling = dict(SAMPLED, max_tokens=20)
+    monkeypatch.setenv("YUEAR_DECODE", "kernels")
+    want, _, _ = engine.generate_tokens(prefix, sampling, 77)
+    monkeypatch.setenv("YUEAR_DECODE", "persistent")
+    got, timing, _ = engine.generate_tokens(prefix, sampling, 77)
+    assert got == want and timing["execution"] == "hip_graph"
+
+
+def test_decode_step_timing_restores_positions(engine):
+    rng = np.random.default_rng(10)
+    prompt = rng.integers(0, 83968, size=30).tolist()
+    tok = int(rng.integers(0, 83968))
+    s = engine.session(1, 64)
+    s.decode_path = "persistent"
+    s.prefill(0, prompt)
+    ms = s.time_kernel("decode_step", 5)
+    assert ms > 0 and s.position(0) == 30
+    got = s.step(tok)
+    s.close()
+    r = engine.session(1, 64)
+    r.prefill(0, prompt)
+    np.testing.assert_array_equal(got, r.step(tok))
+    r.close()
+
+
+def test_expired_wait_is_reported(engine, monkeypatch):
+    # A spin limit of 0 makes every dependency wait that is not already
+    # satisfied on its first poll give up: the kernel still runs to its end
+    # (all reads stay in bounds whatever the activations hold) and the host
+    # must report the expired wait instead of returning the logits.
+    monkeypatch.setenv("YUEAR_DECODE_SPIN_LIMIT", "0")
+    s = engine.session(1, 32)
+    s.decode_path = "persistent"
+    s.prefill(0, [1, 2, 3])
+    with pytest.raises(RuntimeError, match="dependency wait expired"):
+        s.step(4)
+    s.close()
+    monkeypatch.delenv("YUEAR_DECODE_SPIN_LIMIT")
+    a = engine.session(1, 32)
+    a.decode_path = "persistent"
+    a.prefill(0, [1, 2, 3])
+    b = engine.session(1, 32)
+    b.prefill(0, [1, 2, 3])
+    np.testing.assert_array_equal(a.step(4), b.step(4))
+    a.close()
+    b.close()

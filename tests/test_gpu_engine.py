@@ -1,5 +1,5 @@
 """Engine / session / generate_tokens on the GPU vs the oracle and the golden
-vectors (tiny model of the BASELINE layer family, one BASELINE-shaped layer).
+vectors (tiny model of the 3B layer family, one 3B-shaped layer).
 
 Reference behaviour restated: vendor/yue/tests/test_cuda_graph.py:38-115
 (decode-step equations, cache poisoning, branch isolation, lifecycle,
@@ -15,7 +15,7 @@ from conftest import ROOT, TINY
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(ROOT, "tests", "golden")
-ATOL, RTOL = 2e-2, 1e-2  # north star logits tolerance (bf16, fp32 accumulate)
+ATOL, RTOL = 2e-2, 1e-2  # logits tolerance of the decode path (bf16, fp32 accumulate)
 
 
 def f(b):
@@ -237,8 +237,8 @@ def test_end_token_and_min_tokens_in_semantic_phase(yuear_lib):
     assert timing["output_tokens"] == 6 and timing["content_tokens"] == 5
 
 
-def test_baseline_layer_step_matches_oracle_and_golden(yuear_lib, oracle):
-    # config 1: one 3072-wide layer, KV N(0,1) over 511 slots, input N(0,1)
+def test_3b_layer_step_matches_oracle_and_golden(yuear_lib, oracle):
+    # one 3072-wide layer, KV N(0,1) over 511 slots, input N(0,1)
     from make_golden import LAYER
     g = np.load(os.path.join(GOLDEN, "layer_3072.npz"))
     seed, length = int(g["seed"]), int(g["length"])

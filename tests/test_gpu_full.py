@@ -1,4 +1,4 @@
-"""The BASELINE 3B decoder at full size on the GPU vs the oracle.
+"""The 3B AR decoder at full size on the GPU vs the oracle.
 
 28 layers, hidden 3072, 24/8 heads, FFN 8192, vocab 83968, N(0, 0.02)
 weights with unit norm gains (the bench's model).
@@ -11,13 +11,13 @@ rule (tools/limits.py:21-79, tools/fidelity.py:124-148): the GPU's distance to
 the higher-precision anchor (oracle, fp64 accumulation) must stay within
 twice the distance of the bf16/fp32 oracle to that anchor, in max_abs and in
 rms, with the cosine and the argmax checked too. The strict 2e-2/1e-2 logit
-tolerance is asserted where it holds (tiny model, single BASELINE layer:
+tolerance is asserted where it holds (tiny model, single 3B layer:
 test_gpu_engine.py).
 """
 import numpy as np
 import pytest
 
-from conftest import BASE_3B
+from conftest import MODEL_3B
 
 pytestmark = pytest.mark.gpu
 
@@ -46,9 +46,9 @@ def check_fidelity(gpu, oracle32, oracle64):
 
 @pytest.fixture(scope="module")
 def pair(yuear_lib, oracle):
-    w = yuear_lib.random_weights(BASE_3B, 20251201)
-    engine = yuear_lib.Engine(BASE_3B, w)
-    model = oracle.Model(BASE_3B, w)
+    w = yuear_lib.random_weights(MODEL_3B, 20251201)
+    engine = yuear_lib.Engine(MODEL_3B, w)
+    model = oracle.Model(MODEL_3B, w)
     yield engine, model, oracle
     oracle.lib().oracle_set_accumulation(0)
     engine.close()
@@ -86,7 +86,7 @@ def test_full_model_decode_at_kv_4096(pair):
     prefix = rng.integers(0, 83968, size=4095).tolist()
     s = engine.session(1, 4100)
     s.prefill(0, prefix)
-    kv = [s.read_kv(layer, 0, 4095) for layer in range(BASE_3B["num_hidden_layers"])]
+    kv = [s.read_kv(layer, 0, 4095) for layer in range(MODEL_3B["num_hidden_layers"])]
     token = int(rng.integers(0, 83968))
     gpu = s.step(token)[0]  # L = 4096
     k_new = s.read_kv(0, 0, 4096)[0][:, 4095]

@@ -4,7 +4,7 @@ The sampler (CFG merge, distribution(), draw) is integer/ordering logic plus
 fp32 arithmetic whose every step is defined on both sides with the same
 operations (portable exp/log, sequential sums in sorted order, Philox
 uniforms), so the drawn token must be bit-identical to the oracle's
-(north star: "a bit-exact sampled token stream when both sides are fed
+(the acceptance bar: "a bit-exact sampled token stream when both sides are fed
 identical uniform draws").
 """
 import numpy as np

@@ -222,7 +222,7 @@ def test_tiny_golden_detects_a_dropped_qk_norm(oracle):
     assert not close(got, f(g["logits_bf16"][0])).all()
 
 
-def test_baseline_layer_matches_torch_golden(oracle):
+def test_3b_layer_matches_torch_golden(oracle):
     import yuear
     from make_golden import LAYER
     g = np.load(os.path.join(GOLDEN, "layer_3072.npz"))

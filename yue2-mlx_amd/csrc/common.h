@@ -152,7 +152,9 @@ __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
 // q/k RMSNorm over a 128-wide head (ar.cpp:268-275, 30-35) followed by the
 // half-split RoPE (ar.cpp:52-87), one head per wave, lane l holding dims
 // 2l and 2l+1; cs/sn point at the bf16 cos/sin row of the position.
-__device__ __forceinline__ void norm_rope_head(float x0, float x1, const uint16_t *gain,
+// (GainPtr: a plain or an address-space-qualified pointer to the [D] gain.)
+template <class GainPtr>
+__device__ __forceinline__ void norm_rope_head(float x0, float x1, GainPtr gain,
                                                float eps, const uint16_t *cs,
                                                const uint16_t *sn, int lane, float &y0,
                                                float &y1) {

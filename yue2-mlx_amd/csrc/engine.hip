@@ -30,6 +30,7 @@
 
 #include "../../include/yuear.h"
 #include "common.h"
+#include "decode.h"
 #include "kernels.h"
 
 namespace yuear {
@@ -325,6 +326,16 @@ struct yuear_session {
   int32_t *pin_tok = nullptr;
   uint16_t *pin_logits = nullptr;
   std::vector<void *> allocations;
+  // persistent decode step (decode.hip): one launch per token
+  int decode_path = 0;  // YUEAR_DECODE_KERNELS or YUEAR_DECODE_PERSISTENT
+  int decode_grid = 0;  // co-resident workgroups; 0: shape not supported
+  int decode_spins = 1 << 20;  // bounded-wait polls (YUEAR_DECODE_SPIN_LIMIT)
+  int32_t *dsync = nullptr;     // counters + error word, zero between launches
+  DecodeLayer *dlayers = nullptr;
+  // activation words of the persistent step (decode.h)
+  uint32_t *dxs = nullptr, *dqkv = nullptr, *dattn = nullptr, *dact = nullptr;
+  uint32_t *dpart_o = nullptr, *dpart_ml = nullptr;
+  int32_t *pin_err = nullptr;
   hipGraphExec_t step_exec = nullptr;
   hipGraph_t step_graph = nullptr;
   hipGraphExec_t gen_exec = nullptr;  // sampler + step, for timed loops
@@ -340,6 +351,7 @@ struct yuear_session {
     for (void *p : allocations) (void)hipFree(p);
     if (pin_tok) (void)hipHostFree(pin_tok);
     if (pin_logits) (void)hipHostFree(pin_logits);
+    if (pin_err) (void)hipHostFree(pin_err);
     if (stream) (void)hipStreamDestroy(stream);
   }
   template <class T> T *alloc(size_t n) {
@@ -554,6 +566,49 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_tok), size_t(kContext + 16) * 4));
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_logits),
                      size_t(branches) * S.phase.stride() * 2));
+  HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_err), 4));
+  // persistent decode step: needs every workgroup of its grid resident at
+  // once; the grid is sized from the occupancy query (YUEAR_DECODE_WG_PER_CU
+  // caps the workgroups per CU, default 2)
+  const int occ = decode_occupancy(c.H, c.F, c.Hq, c.Hkv, branches);
+  if (occ > 0) {
+    int cus = 0;
+    HIPC(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, E->device));
+    int per_cu = 2;
+    if (const char *env = std::getenv("YUEAR_DECODE_WG_PER_CU"))
+      per_cu = std::max(1, std::atoi(env));
+    S.decode_grid = std::min(per_cu, occ) * cus;
+    if (const char *env = std::getenv("YUEAR_DECODE_SPIN_LIMIT"))
+      S.decode_spins = std::max(0, std::atoi(env));
+    const size_t words = decode_sync_words(c.layers);
+    S.dsync = S.alloc<int32_t>(words);
+    HIPC(hipMemsetAsync(S.dsync, 0, words * 4, S.stream));
+    const size_t L = c.layers, Bn = branches;
+    const size_t parts = Bn * c.Hkv * S.max_splits * G;
+    // zero words carry tag 0, which no launch uses
+    const size_t act_words = (2 * L + 1) * Bn * c.H + L * Bn * (c.qkv() + c.Hq * c.D + c.F) +
+                             L * parts * (2 * c.D + 4);
+    uint32_t *act_base = S.alloc<uint32_t>(act_words);
+    HIPC(hipMemsetAsync(act_base, 0, act_words * 4, S.stream));
+    S.dxs = act_base;
+    S.dqkv = S.dxs + (2 * L + 1) * Bn * c.H;
+    S.dattn = S.dqkv + L * Bn * c.qkv();
+    S.dact = S.dattn + L * Bn * c.Hq * c.D;
+    S.dpart_o = S.dact + L * Bn * c.F;
+    S.dpart_ml = S.dpart_o + L * parts * 2 * c.D;
+    std::vector<DecodeLayer> table(c.layers);
+    for (int l = 0; l < c.layers; ++l) {
+      const LayerW &L = E->layers[l];
+      table[l] = DecodeLayer{L.input_ln, L.post_ln, c.qk_norm ? L.q_norm : nullptr,
+                             c.qk_norm ? L.k_norm : nullptr, L.qkv, L.o, L.gu, L.down};
+    }
+    S.dlayers = S.alloc<DecodeLayer>(c.layers);
+    HIPC(hipMemcpyAsync(S.dlayers, table.data(), table.size() * sizeof(DecodeLayer),
+                        hipMemcpyHostToDevice, S.stream));
+    const char *env = std::getenv("YUEAR_DECODE");
+    S.decode_path = env && std::string(env) == "persistent" ? YUEAR_DECODE_PERSISTENT
+                                                            : YUEAR_DECODE_KERNELS;
+  }
   HIPC(hipStreamSynchronize(S.stream));
 }
 
@@ -717,8 +772,36 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
   HIPC(launch_gemv(g, S.stream));
 }
 
+DecodeParams decode_params(yuear_session &S) {
+  yuear_engine &E = *S.e;
+  const Config &c = E.cfg;
+  DecodeParams p;
+  p.H = c.H; p.F = c.F; p.Hq = c.Hq; p.Hkv = c.Hkv; p.B = S.B; p.n_layers = c.layers;
+  p.vocab = c.V;
+  p.eps = c.eps;
+  p.attn_scale = float(std::pow(double(c.D), -0.5));  // ar.cpp:283
+  p.embed = E.embed; p.lm_head = E.lm_head; p.final_norm = E.final_norm;
+  p.rope_cos = E.rope_cos; p.rope_sin = E.rope_sin;
+  p.layers = S.dlayers;
+  p.kc = S.kc; p.vc = S.vc; p.cap = S.cap;
+  p.pos = S.pos; p.tok = S.tok;
+  p.xs = S.dxs; p.qkv = S.dqkv; p.qkv_stride = c.qkv(); p.attn = S.dattn; p.act = S.dact;
+  p.part_o = S.dpart_o; p.part_ml = S.dpart_ml; p.max_splits = S.max_splits;
+  p.logits = S.logits; p.ls = S.phase.stride(); p.n_logits = S.phase.size;
+  p.seg0_start = S.phase.seg0_start; p.seg0_len = S.phase.seg0_len;
+  p.seg1_start = S.phase.seg1_start;
+  p.sync = S.dsync;
+  p.grid = S.decode_grid;
+  p.max_spins = S.decode_spins;
+  return p;
+}
+
 // whole decode step: tok -> logits, pos += 1
 void enqueue_step(yuear_session &S) {
+  if (S.decode_path == YUEAR_DECODE_PERSISTENT) {
+    HIPC(launch_decode_step(decode_params(S), S.stream));
+    return;
+  }
   for (int l = 0; l < S.e->cfg.layers; ++l)
     enqueue_layer(S, l, l == 0);
   enqueue_head(S, S.x, S.B, S.e->cfg.H, S.logits, S.pos);
@@ -738,6 +821,39 @@ void ensure_step_graph(yuear_session &S) {
   }
   HIPC(hipStreamEndCapture(S.stream, &S.step_graph));
   HIPC(hipGraphInstantiate(&S.step_exec, S.step_graph, nullptr, nullptr, 0));
+}
+
+// The persistent step reports an expired dependency wait through a sticky
+// word (its workgroups were not all resident): the results since the last
+// check are invalid. Synchronises the session stream.
+void check_decode(yuear_session &S) {
+  if (!S.dsync)
+    return;
+  HIPC(hipMemcpyAsync(S.pin_err, S.dsync + kSyncError, 4, hipMemcpyDeviceToHost, S.stream));
+  HIPC(hipStreamSynchronize(S.stream));
+  if (*S.pin_err != 0) {
+    // reset everything but the epoch (activation words keep their tags)
+    HIPC(hipMemsetAsync(S.dsync, 0, kSyncEpoch * 4, S.stream));
+    HIPC(hipMemsetAsync(S.dsync + kSyncEpoch + 1, 0,
+                        (decode_sync_words(S.e->cfg.layers) - kSyncEpoch - 1) * 4, S.stream));
+    HIPC(hipStreamSynchronize(S.stream));
+    throw Error("RuntimeError",
+                "persistent decode step: a dependency wait expired (workgroups not co-resident); "
+                "the decoded state is invalid");
+  }
+}
+
+void drop_graphs(yuear_session &S) {
+  HIPC(hipStreamSynchronize(S.stream));
+  if (S.step_exec) (void)hipGraphExecDestroy(S.step_exec);
+  if (S.step_graph) (void)hipGraphDestroy(S.step_graph);
+  if (S.gen_exec) (void)hipGraphExecDestroy(S.gen_exec);
+  if (S.gen_graph) (void)hipGraphDestroy(S.gen_graph);
+  S.step_exec = nullptr;
+  S.step_graph = nullptr;
+  S.gen_exec = nullptr;
+  S.gen_graph = nullptr;
+  S.gen_key.clear();
 }
 
 void check_tokens(const int32_t *ids, int n, int vocab) {  // sampling.cpp:139-146
@@ -845,10 +961,12 @@ void step(yuear_session &S, const int32_t *tokens, uint16_t *logits_out) {
     HIPC(hipMemcpyAsync(S.pin_logits, S.logits, size_t(S.B) * ls * 2, hipMemcpyDeviceToHost,
                         S.stream));
     HIPC(hipStreamSynchronize(S.stream));
+    check_decode(S);
     for (int b = 0; b < S.B; ++b)
       std::memcpy(logits_out + b * n, S.pin_logits + b * ls, n * 2);
   } else {
     HIPC(hipStreamSynchronize(S.stream));
+    check_decode(S);
   }
 }
 
@@ -1075,6 +1193,55 @@ yuear_status yuear_session_set_position(yuear_session *S, int32_t branch, int32_
   });
 }
 
+yuear_status yuear_session_set_decode_path(yuear_session *S, int32_t path, char **error_json) {
+  return guarded(error_json, [&] {
+    if (!S || (path != YUEAR_DECODE_KERNELS && path != YUEAR_DECODE_PERSISTENT))
+      invalid("decode path must be YUEAR_DECODE_KERNELS or YUEAR_DECODE_PERSISTENT");
+    if (path == YUEAR_DECODE_PERSISTENT && !S->dsync)
+      invalid("the persistent decode step is not available for this model shape / branch count");
+    if (path != S->decode_path) {
+      drop_graphs(*S);
+      S->decode_path = path;
+    }
+  });
+}
+
+int32_t yuear_session_decode_path(const yuear_session *S) { return S ? S->decode_path : -1; }
+
+yuear_status yuear_session_trace_step(yuear_session *S, uint64_t *trace_out, int64_t capacity,
+                                      int32_t *grid_out, char **error_json) {
+  return guarded(error_json, [&] {
+    if (!S || !trace_out || !grid_out)
+      invalid("session and outputs are required");
+    if (!S->dsync)
+      invalid("the persistent decode step is not available for this session");
+    for (int b = 0; b < S->B; ++b)
+      if (S->host_pos[b] + 1 > S->cap)
+        invalid("trace_step needs a free slot");
+    const size_t n = (size_t(S->e->cfg.layers) * kPhases + 1) * S->decode_grid * 2;
+    if (capacity < int64_t(n))
+      invalid("trace buffer too small: need " + std::to_string(n) + " entries");
+    DecodeParams dp = decode_params(*S);
+    unsigned long long *dev = nullptr;
+    HIPC(hipMalloc(&dev, n * 8));
+    const auto release = [&] { (void)hipFree(dev); };
+    try {
+      HIPC(hipMemsetAsync(dev, 0, n * 8, S->stream));
+      dp.trace = dev;
+      HIPC(launch_decode_step(dp, S->stream));
+      HIPC(hipStreamSynchronize(S->stream));
+      HIPC(hipMemcpy(trace_out, dev, n * 8, hipMemcpyDeviceToHost));
+      set_device_pos(*S);  // the traced step leaves the positions unchanged
+      check_decode(*S);
+    } catch (...) {
+      release();
+      throw;
+    }
+    release();
+    *grid_out = S->decode_grid;
+  });
+}
+
 yuear_status yuear_session_layer_step(yuear_session *S, int32_t layer, const uint16_t *x_in,
                                       uint16_t *x_out, char **error_json) {
   return guarded(error_json, [&] {
@@ -1120,6 +1287,7 @@ yuear_status yuear_session_time_steps(yuear_session *S, int32_t steps, double *m
     (void)hipEventDestroy(e1);
     for (int b = 0; b < S->B; ++b)
       S->host_pos[b] += steps;
+    check_decode(*S);
     *ms_per_step = double(ms) / steps;
   });
 }
@@ -1186,6 +1354,7 @@ yuear_status yuear_session_time_generate(yuear_session *S, const yuear_sampling 
     (void)hipEventDestroy(e1);
     for (int b = 0; b < S->B; ++b)
       S->host_pos[b] += steps;
+    check_decode(*S);
     *ms_per_step = double(ms) / steps;
     if (tokens_out)
       HIPC(hipMemcpy(tokens_out, S->history + first, size_t(steps) * 4, hipMemcpyDeviceToHost));
@@ -1201,6 +1370,35 @@ yuear_status yuear_session_time_kernel(yuear_session *S, const char *kernel, int
     for (int b = 0; b < S->B; ++b)
       if (which == "attention" && S->host_pos[b] >= S->cap)
         invalid("attention timing needs a free slot");
+    if (which == "decode_step") {
+      // back-to-back persistent steps from the current positions; the
+      // positions are restored afterwards (the slots written stay invisible)
+      if (!S->dsync)
+        invalid("the persistent decode step is not available for this session");
+      for (int b = 0; b < S->B; ++b)
+        if (S->host_pos[b] + launches + 1 > S->cap)
+          invalid("decode_step timing needs launches + 1 free slots");
+      const DecodeParams dp = decode_params(*S);
+      HIPC(launch_decode_step(dp, S->stream));
+      HIPC(hipStreamSynchronize(S->stream));
+      set_device_pos(*S);
+      hipEvent_t e0, e1;
+      HIPC(hipEventCreate(&e0));
+      HIPC(hipEventCreate(&e1));
+      HIPC(hipEventRecord(e0, S->stream));
+      for (int i = 0; i < launches; ++i)
+        HIPC(launch_decode_step(dp, S->stream));
+      HIPC(hipEventRecord(e1, S->stream));
+      HIPC(hipEventSynchronize(e1));
+      float ms = 0.f;
+      HIPC(hipEventElapsedTime(&ms, e0, e1));
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+      set_device_pos(*S);
+      check_decode(*S);
+      *ms_per_launch = double(ms) / launches;
+      return;
+    }
     enqueue_one(*S, which, 0);  // validates the name, warms the code object
     HIPC(hipStreamSynchronize(S->stream));
     hipEvent_t e0, e1;
@@ -1345,6 +1543,7 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
     while (consumed < launched && !eos && !cancelled)
       consume();
     HIPC(hipStreamSynchronize(S->stream));
+    check_decode(*S);
     if (cancelled)
       throw Error("InterruptedError", "Cancelled during " + phase);
     const double seconds = since(t0);
