@@ -9,18 +9,16 @@
 // from HBM exactly once per step. The chunk length is derived on device from
 // pos[b], so one captured graph serves every KV length up to capacity.
 //
-// Prologue: every workgroup normalises and rotates its G query heads and the
-// current key in registers (q_norm/k_norm and the half-split RoPE with the
-// reference's bf16 rounding points); the workgroup whose range contains slot
-// pos[b] appends the new K/V to the cache and takes that key from LDS.
-//
-// Main loop: 64 keys per pass, 16 per wave; a 16-lane group reads one 256-byte
-// key row per 16-byte lane load, four rows per wave-wide load (1 KiB
-// contiguous). Online softmax in fp32 (exp2 with log2(e) folded into q).
-// Partials (m, l, o) go to a global buffer; the last workgroup to arrive on a
+// The per-split math (prologue, passes, online softmax, wave combine) is
+// attn_core.h, shared with the persistent step. Here: the q/k/v inputs are
+// issued first, then the split's first 128-key pass of K/V, so the prologue
+// (q/k RMSNorm + RoPE) overlaps the K/V stream; the workgroup whose range
+// contains slot pos[b] appends the new K/V. Partials (m, l, o) go to a
+// global buffer with write-through stores; the last workgroup to arrive on a
 // kv head (device-scope counter) merges the splits exactly and writes bf16.
 #include <cmath>
 
+#include "attn_core.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -28,16 +26,7 @@ namespace yuear {
 
 namespace {
 
-constexpr int D = 128;
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ void unpack8(u32x4 v, float *f) {
-  f[0] = bflo(v.x); f[1] = bfhi(v.x);
-  f[2] = bflo(v.y); f[3] = bfhi(v.y);
-  f[4] = bflo(v.z); f[5] = bfhi(v.z);
-  f[6] = bflo(v.w); f[7] = bfhi(v.w);
-}
-
+constexpr int D = attn::D;
 constexpr int kMaxSplits = 64;
 
 // s_waitcnt vmcnt(0): this wave's outstanding vector memory operations
@@ -50,26 +39,10 @@ __device__ __forceinline__ float coherent_load(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void load_tile(const u32x4 *kc, const u32x4 *vc, int t0, int wave,
-                                          int grp, int sub, int last_cached, u32x4 *kr,
-                                          u32x4 *vr) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // keys at or beyond the current slot come from LDS (or are masked); the
-    // clamp keeps every address inside the written part of the cache
-    const int kk = min(t0 + wave * 16 + i * 4 + grp, last_cached);
-    kr[i] = kc[size_t(kk) * (D / 8) + sub];
-    vr[i] = vc[size_t(kk) * (D / 8) + sub];
-  }
-}
-
 template <int G>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, float scale) {
-  __shared__ float q_lds[G][D];        // scaled query (fp32), log2(e) folded in
-  __shared__ u32x4 kv_new[2][D / 8];   // current key / value (bf16)
-  __shared__ float w_m[4][G], w_l[4][G];
-  __shared__ float w_o[4][G][D];
-  __shared__ float s_m[kMaxSplits][G], s_w[kMaxSplits][G], s_den[G];
+  __shared__ attn::Lds<G> sh;
+  __shared__ float s_w[kMaxSplits][G];  // merge weights
   __shared__ int is_last;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -91,160 +64,51 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
   if (active) {
     const int grp = lane >> 4, sub = lane & 15;
     const int last_cached = pos > 0 ? pos - 1 : 0;
-    // first K/V tile in flight before the prologue's dependent work
-    u32x4 kr[4], vr[4];
-    load_tile(kc, vc, s0, wave, grp, sub, last_cached, kr, vr);
+    // q/k/v inputs of this wave's heads (h = wave, wave + 4 < G + 2) first,
+    // then the first pass of K/V: the prologue waits only for the former
+    const uint16_t *row = p.qkv + size_t(b) * p.qkv_stride;
+    uint32_t pair[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = min(wave + 4 * j, G + 1);
+      const size_t col = h < G ? size_t(kvh * G + h) * D
+                               : size_t(p.heads + (h - G) * Hkv + kvh) * D;
+      pair[j] = reinterpret_cast<const uint32_t *>(row + col)[lane];
+    }
+    u32x4 kr[attn::kRows], vr[attn::kRows];
+    attn::load_k(kc, s0, wave, grp, sub, last_cached, kr);
+    attn::load_v(vc, s0, wave, grp, sub, last_cached, vr);
 
     // ---- prologue: q heads, current k, current v ----
-    const uint16_t *row = p.qkv + size_t(b) * p.qkv_stride;
     const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
     const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
-    for (int h = wave; h < G + 2; h += 4) {
-      const uint16_t *src;
-      if (h < G)
-        src = row + size_t(kvh * G + h) * D;
-      else if (h == G)
-        src = row + size_t(p.heads) * D + size_t(kvh) * D;
-      else
-        src = row + size_t(p.heads + Hkv) * D + size_t(kvh) * D;
-      const uint32_t pair = reinterpret_cast<const uint32_t *>(src)[lane];
-      float y0 = bflo(pair), y1 = bfhi(pair);
-      if (h <= G)
-        norm_rope_head(y0, y1, h < G ? p.q_norm : p.k_norm, p.eps, cs, sn, lane, y0, y1);
-      if (h < G) {
-        q_lds[h][2 * lane] = y0 * (scale * kLog2e);
-        q_lds[h][2 * lane + 1] = y1 * (scale * kLog2e);
-      } else {
-        reinterpret_cast<uint32_t *>(&kv_new[h - G][0])[lane] =
-            uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
-      }
+    const float qscale = scale * attn::kLog2e;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = wave + 4 * j;
+      if (h < G + 2)
+        attn::prologue_head<G>(sh, h, pair[j], h < G ? p.q_norm : p.k_norm, p.eps, cs, sn,
+                               qscale, lane);
     }
     __syncthreads();
     if (pos >= s0 && pos < s1 && threadIdx.x < 2 * (D / 8)) {  // append (ar.cpp:119-123)
       const int which = threadIdx.x / (D / 8), c = threadIdx.x % (D / 8);
       u32x4 *dst = reinterpret_cast<u32x4 *>(which ? p.v_cache : p.k_cache) +
                    (head_base + pos) * (D / 8) + c;
-      *dst = kv_new[which][c];
+      *dst = sh.kv_new[which][c];
     }
 
-    // ---- main loop: 64 keys per pass, next tile prefetched ----
-    float q[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        q[h][e] = q_lds[h][sub * 8 + e];
-    float m_run[G], l_run[G], o_run[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      m_run[h] = -__builtin_inff();
-      l_run[h] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        o_run[h][e] = 0.f;
-    }
-    for (int t0 = s0; t0 < s1; t0 += 64) {
-      u32x4 kn[4], vn[4];
-      load_tile(kc, vc, t0 + 64, wave, grp, sub, last_cached, kn, vn);
-      float sc[4][G];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = t0 + wave * 16 + i * 4 + grp;
-        if (key == pos) {
-          kr[i] = kv_new[0][sub];
-          vr[i] = kv_new[1][sub];
-        }
-        float kf[8];
-        unpack8(kr[i], kf);
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          float acc = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            acc = fmaf(q[h][e], kf[e], acc);
-          acc += __shfl_xor(acc, 8, 64);
-          acc += __shfl_xor(acc, 4, 64);
-          acc += __shfl_xor(acc, 2, 64);
-          acc += __shfl_xor(acc, 1, 64);
-          sc[i][h] = key < s1 ? acc : -__builtin_inff();
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run[h], mx);
-        if (m_new == -__builtin_inff())
-          continue;  // nothing visible yet in this wave
-        const float corr = __builtin_amdgcn_exp2f(m_run[h] - m_new);
-        float lsum = 0.f;
-        float pw[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pw[i] = __builtin_amdgcn_exp2f(sc[i][h] - m_new);
-          lsum += pw[i];
-        }
-        l_run[h] = l_run[h] * corr + lsum;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          o_run[h][e] *= corr;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float vf[8];
-          unpack8(vr[i], vf);
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            o_run[h][e] = fmaf(pw[i], vf[e], o_run[h][e]);
-        }
-        m_run[h] = m_new;
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kr[i] = kn[i];
-        vr[i] = vn[i];
-      }
-    }
-    // reduce the four 16-lane groups of the wave
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float l = l_run[h];
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float o = o_run[h][e];
-        o += __shfl_xor(o, 16, 64);
-        o += __shfl_xor(o, 32, 64);
-        o_run[h][e] = o;
-      }
-      if (lane < 16) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          w_o[wave][h][sub * 8 + e] = o_run[h][e];
-      }
-      if (lane == 0) {
-        w_m[wave][h] = m_run[h];
-        w_l[wave][h] = l;
-      }
-    }
+    // ---- passes over the split, then the 4-wave combine ----
+    attn::split<G>(sh, kc, vc, s0, s1, pos, last_cached, lane, wave, kr, vr);
     __syncthreads();
-    // merge the four waves; write the split partial
     for (int e = threadIdx.x; e < G * D; e += 256) {
-      const int h = e / D, d = e % D;
-      float M = fmaxf(fmaxf(w_m[0][h], w_m[1][h]), fmaxf(w_m[2][h], w_m[3][h]));
-      float o = 0.f, l = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float f = w_m[w][h] == -__builtin_inff() ? 0.f
-                                                        : __builtin_amdgcn_exp2f(w_m[w][h] - M);
-        o = fmaf(f, w_o[w][h][d], o);
-        l = fmaf(f, w_l[w][h], l);
-      }
+      float o, M, l;
+      attn::combine<G>(sh, e, o, M, l);
       // write-through (agent-scope) stores: visible to every XCD once complete
       __hip_atomic_store(&p.part_o[(part + s) * (G * D) + e], o, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-      if (d == 0) {
+      if (e % D == 0) {
+        const int h = e / D;
         __hip_atomic_store(&p.part_ml[((part + s) * G + h) * 2], M, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&p.part_ml[((part + s) * G + h) * 2 + 1], l, __ATOMIC_RELAXED,
@@ -269,58 +133,48 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
   if (!is_last)
     return;
   const int n_active = (L + chunk - 1) / chunk;
-  // One memory round: this thread's partial-o loads (up to kMergeBatch splits
-  // per output) are issued together with the (m, l) staging loads.
-  constexpr int kMergeBatch = 32;
-  constexpr int kOutPerThread = (G * D + 255) / 256;
-  float ov[kOutPerThread][kMergeBatch];
+  // One memory round: thread x owns outputs (2 q, 2 q + 1), q = x + 256 r, and
+  // issues the 8-byte partial loads of all its splits up front (clamped to
+  // the active ones); meanwhile wave h turns the (m, l) of head h into merge
+  // weights, lane t for split t.
+  constexpr int kPairs = G * D / 2;
+  constexpr int kRounds = (kPairs + 255) / 256;
+  for (int r = 0; r < kRounds; ++r) {
+    const int q = min(int(threadIdx.x) + 256 * r, kPairs - 1);
+    const unsigned long long *po =
+        reinterpret_cast<const unsigned long long *>(p.part_o + part * (G * D)) + q;
+    unsigned long long ov[kMaxSplits];
 #pragma unroll
-  for (int r = 0; r < kOutPerThread; ++r) {
-    const int e = min(int(threadIdx.x) + 256 * r, G * D - 1);
-    const float *po = p.part_o + part * (G * D) + e;
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j)
-      ov[r][j] = coherent_load(po + size_t(min(j, n_active - 1)) * (G * D));
-  }
-  for (int i = threadIdx.x; i < n_active * G; i += 256) {
-    const int t = i / G, h = i - t * G;
-    s_m[t][h] = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
-    s_w[t][h] = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);  // l, made a weight below
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int h = threadIdx.x;
-    float M = -__builtin_inff();
-    for (int t = 0; t < n_active; ++t)
-      M = fmaxf(M, s_m[t][h]);
-    float den = 0.f;
-    for (int t = 0; t < n_active; ++t) {
-      const float f = s_m[t][h] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(s_m[t][h] - M);
-      s_m[t][h] = f;
-      den = fmaf(f, s_w[t][h], den);
+    for (int j = 0; j < kMaxSplits; ++j)
+      ov[j] = __hip_atomic_load(po + size_t(min(j, n_active - 1)) * (G * D / 2), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+    if (r == 0) {
+      for (int h = wave; h < G; h += 4) {
+        const bool act = lane < n_active;
+        const int t = act ? lane : 0;
+        const float m = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
+        const float l = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);
+        const float w = merge_weight(m, l, act);
+        if (act)
+          s_w[lane][h] = w;
+      }
+      __syncthreads();
     }
-    s_den[h] = den;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < n_active * G; i += 256) {
-    const int t = i / G, h = i - t * G;
-    s_w[t][h] = s_m[t][h] / s_den[h];
-  }
-  __syncthreads();
+    if (int(threadIdx.x) + 256 * r < kPairs) {
+      const int h = (2 * q) / D;
+      float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-  for (int r = 0; r < kOutPerThread; ++r) {
-    const int e = int(threadIdx.x) + 256 * r;
-    if (e >= G * D)
-      break;
-    const int h = e / D;
-    const float *po = p.part_o + part * (G * D) + e;
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j)
-      acc = j < n_active ? fmaf(s_w[j][h], ov[r][j], acc) : acc;
-    for (int t = kMergeBatch; t < n_active; ++t)  // more than kMergeBatch splits
-      acc = fmaf(s_w[t][h], coherent_load(po + size_t(t) * (G * D)), acc);
-    p.out[size_t(b) * p.out_stride + size_t(kvh * G) * D + e] = f2bf(acc);
+      for (int j = 0; j < kMaxSplits; ++j) {
+        if (j < n_active) {  // sequential over splits
+          const float o0 = __builtin_bit_cast(float, uint32_t(ov[j]));
+          const float o1 = __builtin_bit_cast(float, uint32_t(ov[j] >> 32));
+          a0 = fmaf(s_w[j][h], o0, a0);
+          a1 = fmaf(s_w[j][h], o1, a1);
+        }
+      }
+      reinterpret_cast<uint32_t *>(p.out + size_t(b) * p.out_stride + size_t(kvh * G) * D)[q] =
+          uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);
+    }
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&p.counters[b * Hkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

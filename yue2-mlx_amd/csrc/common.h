@@ -122,18 +122,90 @@ YHD float portable_exp(float x) {
 YHD float gumbel(float u) { return -portable_log(-portable_log(u)); }
 
 #if defined(__HIP__)  // HIP translation units (host and device passes)
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-    v += __shfl_xor(v, o, 64);
+// Cross-lane reductions without the LDS crossbar (ds_bpermute costs an LDS
+// round trip per step, and the decode kernels run one wave per SIMD, so
+// nothing hides it): DPP permutations inside 16-lane rows, then the gfx950
+// v_permlane16_swap / v_permlane32_swap across rows. Every lane of the
+// reduced group receives bit-identical results (each step adds the same two
+// operands on both sides).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum / max over the 16 lanes of a row.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp<0x141>(v);  // row_half_mirror: the other quad of the half-row
+  v += dpp<0x140>(v);  // row_mirror: the other half of the row
   return v;
+}
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+// v_permlane16_swap_b32 a, b swaps the odd rows of a with the even rows of
+// b; v_permlane32_swap_b32 a, b swaps the high half of a with the low half of
+// b. With a = b = v on entry:
+//   permlane16: a = rows (0,0,2,2) of v, b = rows (1,1,3,3);
+//   permlane32: a = low half twice,     b = high half twice.
+// Issued through inline asm with both operands read-write: this compiler's
+// two-result builtins lose the second result when both are added together.
+// The two wait states before match what the compiler emits for the builtin.
+__device__ __forceinline__ void permlane16_swap(uint32_t &a, uint32_t &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(uint32_t &a, uint32_t &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float sum_row_pairs(float v) {  // rows 2k + 2k+1
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane16_swap(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_row_pairs(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane16_swap(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float sum_halves(float v) {  // lanes 0-31 + lanes 32-63
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane32_swap(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_halves(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane32_swap(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+// Value held by lane ^ 32.
+__device__ __forceinline__ float xor32(float v, int lane) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+  permlane32_swap(a, b);
+  return __builtin_bit_cast(float, lane & 32 ? a : b);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  return sum_halves(sum_row_pairs(row_sum16(v)));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-    v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return max_halves(max_row_pairs(row_max16(v)));
 }
+// Split-K merge weight of split t, held by lane t (active: t < n_active):
+// f_t / sum_s f_s l_s with f_t = exp2(m_t - max_s m_s) (log2(e) is folded
+// into the scores) and l_t the split's softmax denominator. Shared by both
+// decode paths so that their merges agree bit for bit.
+__device__ __forceinline__ float merge_weight(float m, float l, bool active) {
+  const float mm = active ? m : -__builtin_inff();
+  const float M = wave_max(mm);
+  const float f = mm == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(mm - M);
+  const float den = wave_sum(active ? f * l : 0.f);
+  return f / den;
+}
+
 // Reinterpret one packed bf16 pair. The element must arrive by value: this
 // clang reads element 0 when __builtin_bit_cast is applied directly to an
 // ext_vector element lvalue such as v.y.
@@ -165,7 +237,7 @@ __device__ __forceinline__ void norm_rope_head(float x0, float x1, GainPtr gain,
     x1 = rbf(rbf(x1 * scale) * bf2f(gain[2 * lane + 1]));
   }
   // ar.cpp:52-87: pair (j, j + D/2); lanes l and l ^ 32 hold the partners.
-  const float p0 = __shfl_xor(x0, 32, 64), p1 = __shfl_xor(x1, 32, 64);
+  const float p0 = xor32(x0, lane), p1 = xor32(x1, lane);
   const int j = (2 * lane) & 63;
   const float c0 = bf2f(cs[j]), c1 = bf2f(cs[j + 1]);
   const float s0 = bf2f(sn[j]), s1 = bf2f(sn[j + 1]);

@@ -49,6 +49,7 @@
 // finish resets the counters, stores the epoch and advances pos.
 #include <cmath>
 
+#include "attn_core.h"
 #include "common.h"
 #include "decode.h"
 #include "kernels.h"
@@ -58,7 +59,6 @@ namespace yuear {
 namespace {
 
 constexpr int D = 128;
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxSplitsP = 64;
 
 // Weight and gain pointers read from the layer table are generic to the
@@ -190,13 +190,6 @@ __device__ __forceinline__ bool wave_settled(bool ok, int spin, const Ctx &cx) {
   return false;
 }
 
-__device__ __forceinline__ void unpack8(u32x4 v, float *f) {
-  f[0] = bflo(v.x); f[1] = bfhi(v.x);
-  f[2] = bflo(v.y); f[3] = bfhi(v.y);
-  f[4] = bflo(v.z); f[5] = bfhi(v.z);
-  f[6] = bflo(v.w); f[7] = bfhi(v.w);
-}
-
 // 8 activation words -> 8 packed bf16 (4 dwords).
 __device__ __forceinline__ u32x4 pack8(u32x4 a, u32x4 b) {
   return u32x4{(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
@@ -207,16 +200,10 @@ __device__ __forceinline__ u32x4 pack8(u32x4 a, u32x4 b) {
 template <int B, int G, int KCMAX>
 union Shared {
   u32x4 xs[B * KCMAX * 64];  // GEMV input rows, bf16 x 8 per chunk
-  struct {
-    float q[G][D];            // scaled query (fp32), log2(e) folded in
-    u32x4 kv_new[2][D / 8];   // current key / value (bf16)
-    float w_m[4][G], w_l[4][G];
-    float w_o[4][G][D];
-  } at;
+  attn::Lds<G> at;            // attention phase
   struct {
     float o[kMaxSplitsP][D];  // partial outputs of one q head
     float m[kMaxSplitsP], w[kMaxSplitsP];
-    float den;
   } mg;
 };
 
@@ -513,9 +500,10 @@ __device__ void gemv_phase(SH &sh, float (*red)[4], const DecodeParams &p, const
   stamp(tr, 1);
 }
 
-// Split-K attention phase of layer l: workgroup tasks (b, kv head, split),
-// the arithmetic of attention.hip's main kernel. Partials are fp32 values
-// stored as two activation words (high half, low half).
+// Split-K attention phase of layer l: workgroup tasks (b, kv head, split)
+// on the shared core (attn_core.h). The split's first K/V pass is issued
+// before the dependency wait; q/k/v come from activation words. Partials are
+// fp32 values stored as two activation words (high half, low half).
 template <int B, int G, class SH>
 __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
                            const DecodeLayer &Lw, const uint32_t *qkv, uint32_t *part_o,
@@ -525,7 +513,7 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
   const int grp = lane >> 4, sub = lane & 15;
   const int Hkv = p.Hkv, S = p.max_splits;
   const int ntasks = B * Hkv * S;
-  const float qscale = p.attn_scale * kLog2e;
+  const float qscale = p.attn_scale * attn::kLog2e;
   const auto qr = rsrc(qkv, uint32_t(B * p.qkv_stride) * 4);
   bool waited = false;
   int done = 0;
@@ -542,13 +530,9 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
     const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.kc) + head_base * (D / 8);
     const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.vc) + head_base * (D / 8);
     const int last_cached = active && pos > 0 ? pos - 1 : 0;
-    u32x4 kr[4], vr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {  // first tile: cached keys only, no dependency
-      const int kk = min(s0 + wave * 16 + i * 4 + grp, last_cached);
-      kr[i] = kc[size_t(kk) * (D / 8) + sub];
-      vr[i] = vc[size_t(kk) * (D / 8) + sub];
-    }
+    u32x4 kr[attn::kRows], vr[attn::kRows];  // first pass: cached keys only, no dependency
+    attn::load_k(kc, s0, wave, grp, sub, last_cached, kr);
+    attn::load_v(vc, s0, wave, grp, sub, last_cached, vr);
     if (!waited) {
       wg_wait(wait_ctr, wait_target, cx);
       waited = true;
@@ -559,30 +543,17 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
       const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
       const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
       for (int h = wave; h < G + 2; h += 4) {
-        uint32_t col;
-        if (h < G)
-          col = uint32_t(kvh * G + h) * D;
-        else if (h == G)
-          col = uint32_t(p.Hq + kvh) * D;
-        else
-          col = uint32_t(p.Hq + Hkv + kvh) * D;
+        const uint32_t col = h < G ? uint32_t(kvh * G + h) * D
+                                   : uint32_t(p.Hq + (h - G) * Hkv + kvh) * D;
         u32x2 pr{};
         for (int spin = 0;; ++spin) {
           pr = ld_w2(qr, (row + col + 2 * lane) * 4);
           if (wave_settled(fresh(pr.x, cx.tag) & fresh(pr.y, cx.tag), spin, cx))
             break;
         }
-        float y0 = bf2f(uint16_t(pr.x)), y1 = bf2f(uint16_t(pr.y));
-        if (h <= G)
-          norm_rope_head(y0, y1, (const GLB uint16_t *)(h < G ? Lw.q_norm : Lw.k_norm), p.eps,
-                         cs, sn, lane, y0, y1);
-        if (h < G) {
-          sh.at.q[h][2 * lane] = y0 * qscale;
-          sh.at.q[h][2 * lane + 1] = y1 * qscale;
-        } else {
-          reinterpret_cast<uint32_t *>(&sh.at.kv_new[h - G][0])[lane] =
-              uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
-        }
+        attn::prologue_head<G>(sh.at, h, (pr.x & 0xffffu) | (pr.y << 16),
+                               (const GLB uint16_t *)(h < G ? Lw.q_norm : Lw.k_norm), p.eps, cs,
+                               sn, qscale, lane);
       }
       __syncthreads();
       if (pos >= s0 && pos < s1 && threadIdx.x < 2 * (D / 8)) {  // append (ar.cpp:119-123)
@@ -591,131 +562,17 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
                      (head_base + pos) * (D / 8) + c;
         *dst = sh.at.kv_new[which][c];
       }
-      float m_run[G], l_run[G], o_run[G][8];
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        m_run[h] = -__builtin_inff();
-        l_run[h] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          o_run[h][e] = 0.f;
-      }
-      // one K and one V buffer: the next tile's keys are issued once the
-      // scores are formed, its values once P.V is done
-      for (int t0 = s0;;) {
-        float sc[4][G];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = t0 + wave * 16 + i * 4 + grp;
-          if (key == pos)
-            kr[i] = sh.at.kv_new[0][sub];
-          float kf[8];
-          unpack8(kr[i], kf);
-#pragma unroll
-          for (int h = 0; h < G; ++h) {
-            const float *q = &sh.at.q[h][sub * 8];  // LDS broadcast within a lane group
-            float acc = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              acc = fmaf(q[e], kf[e], acc);
-            acc += __shfl_xor(acc, 8, 64);
-            acc += __shfl_xor(acc, 4, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 1, 64);
-            sc[i][h] = key < s1 ? acc : -__builtin_inff();
-          }
-        }
-        const bool more = t0 + 64 < s1;  // uniform
-        if (more) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kk = min(t0 + 64 + wave * 16 + i * 4 + grp, last_cached);
-            kr[i] = kc[size_t(kk) * (D / 8) + sub];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (t0 + wave * 16 + i * 4 + grp == pos)
-            vr[i] = sh.at.kv_new[1][sub];
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          const float m_new = fmaxf(m_run[h], mx);
-          if (m_new == -__builtin_inff())
-            continue;
-          const float corr = __builtin_amdgcn_exp2f(m_run[h] - m_new);
-          float lsum = 0.f, pw[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pw[i] = __builtin_amdgcn_exp2f(sc[i][h] - m_new);
-            lsum += pw[i];
-          }
-          l_run[h] = l_run[h] * corr + lsum;
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            o_run[h][e] *= corr;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float vf[8];
-            unpack8(vr[i], vf);
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              o_run[h][e] = fmaf(pw[i], vf[e], o_run[h][e]);
-          }
-          m_run[h] = m_new;
-        }
-        if (!more)
-          break;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kk = min(t0 + 64 + wave * 16 + i * 4 + grp, last_cached);
-          vr[i] = vc[size_t(kk) * (D / 8) + sub];
-        }
-        t0 += 64;
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float lv = l_run[h];
-        lv += __shfl_xor(lv, 16, 64);
-        lv += __shfl_xor(lv, 32, 64);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float o = o_run[h][e];
-          o += __shfl_xor(o, 16, 64);
-          o += __shfl_xor(o, 32, 64);
-          o_run[h][e] = o;
-        }
-        if (lane < 16) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            sh.at.w_o[wave][h][sub * 8 + e] = o_run[h][e];
-        }
-        if (lane == 0) {
-          sh.at.w_m[wave][h] = m_run[h];
-          sh.at.w_l[wave][h] = lv;
-        }
-      }
+      attn::split<G>(sh.at, kc, vc, s0, s1, pos, last_cached, lane, wave, kr, vr);
       __syncthreads();
       const size_t part = (size_t(b) * Hkv + kvh) * S + s;
       for (int e = threadIdx.x; e < G * D; e += 256) {
-        const int h = e / D, d = e % D;
-        const float M = fmaxf(fmaxf(sh.at.w_m[0][h], sh.at.w_m[1][h]),
-                              fmaxf(sh.at.w_m[2][h], sh.at.w_m[3][h]));
-        float o = 0.f, lsum = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float f = sh.at.w_m[w][h] == -__builtin_inff()
-                              ? 0.f
-                              : __builtin_amdgcn_exp2f(sh.at.w_m[w][h] - M);
-          o = fmaf(f, sh.at.w_o[w][h][d], o);
-          lsum = fmaf(f, sh.at.w_l[w][h], lsum);
-        }
+        float o, M, lsum;
+        attn::combine<G>(sh.at, e, o, M, lsum);
         const uint32_t ob = __builtin_bit_cast(uint32_t, o);
         st_w2(part_o + (part * (G * D) + e) * 2, word(cx.tag, ob >> 16),
               word(cx.tag, ob & 0xffffu));
-        if (d == 0) {
+        if (e % D == 0) {
+          const int h = e / D;
           const uint32_t mb = __builtin_bit_cast(uint32_t, M);
           const uint32_t lb = __builtin_bit_cast(uint32_t, lsum);
           st_w2(part_ml + (part * G + h) * 4, word(cx.tag, mb >> 16), word(cx.tag, mb & 0xffffu));
@@ -739,8 +596,8 @@ __device__ __forceinline__ float join(uint32_t hi, uint32_t lo) {
 }
 
 // Merge phase: workgroup tasks (b, q head); the merge arithmetic of
-// attention.hip's last-arriving workgroup (sequential den and sum over
-// splits), one head per task.
+// attention.hip's last-arriving workgroup (merge_weight, then a sequential
+// sum over splits per output), one head per task.
 template <int B, int G, class SH>
 __device__ void merge_phase(SH &sh, const DecodeParams &p, const Ctx &cx,
                             const uint32_t *part_o, const uint32_t *part_ml, uint32_t *attn,
@@ -795,22 +652,13 @@ __device__ void merge_phase(SH &sh, const DecodeParams &p, const Ctx &cx,
             break;
         }
       }
-      if (threadIdx.x == 0) {
-        float M = -__builtin_inff();
-        for (int t = 0; t < n_active; ++t)
-          M = fmaxf(M, sh.mg.m[t]);
-        float den = 0.f;
-        for (int t = 0; t < n_active; ++t) {
-          const float f =
-              sh.mg.m[t] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sh.mg.m[t] - M);
-          sh.mg.m[t] = f;
-          den = fmaf(f, sh.mg.w[t], den);
-        }
-        sh.mg.den = den;
+      if (threadIdx.x < 64) {  // wave 0, lane t: merge weight of split t
+        const int t = threadIdx.x;
+        const bool act = t < n_active;
+        const float w = merge_weight(act ? sh.mg.m[t] : 0.f, act ? sh.mg.w[t] : 0.f, act);
+        if (act)
+          sh.mg.w[t] = w;
       }
-      __syncthreads();
-      if (int(threadIdx.x) < n_active)
-        sh.mg.w[threadIdx.x] = sh.mg.m[threadIdx.x] / sh.mg.den;
       __syncthreads();
       if (threadIdx.x < D) {
         const int d = threadIdx.x;
