@@ -12,6 +12,15 @@ replayed as one hipGraph per token with no host sync between tokens. With
 --decode persistent it is one persistent kernel (same bits, slower today). Inputs (weights, KV cache, logits)
 are resident in HBM when the timed region starts.
 
+Other workloads of the same model (one JSON line each, not the headline):
+  --config cfg     CFG as batch 2 (cond + uncond 512-token prompts), scale 1.5,
+                   T 1.0 / top-k 50 / top-p 0.93, 1024 tokens through the
+                   request driver (yuear_generate_tokens): output tokens/s.
+  --config long    3000-token prefill (TFLOP/s against the bf16 MFMA peak),
+                   then batch-1 decode until KV 8192: ms/token per 512 steps.
+  --config batch8  8 independent sequences, prompts U[128, 2048], capacity
+                   6144, 512 greedy steps each: aggregate tokens/s.
+
 Prints one JSON line on stdout; progress goes to stderr.
 """
 import argparse
@@ -29,6 +38,7 @@ CONFIG = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
               max_position_embeddings=24576, rms_norm_eps=1e-5, rope_theta=500000.0,
               qk_norm=True)
 PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, flop/s
 KV_BYTES_PER_POS = 2 * 8 * 128 * 2 * 28  # K and V, Hkv * D * bf16 * layers
 
 
@@ -57,6 +67,14 @@ def kernel_bytes(c, kernel, kv_len):
     }[kernel]
 
 
+def gemv_shape(c, kernel):
+    """(weight rows, K) of a decode projection."""
+    H, F, V = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
+    qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
+    return {"qkv": (qd + 2 * kd, H), "o_proj": (H, qd), "gate_up": (2 * F, H),
+            "down": (H, F), "lm_head": (V, H)}[kernel]
+
+
 def traffic_from_profiles(kernel):
     """Measured HBM bytes per launch, if a PMC summary has been committed."""
     name = "decode_step_3b_kv4096_pmc.md" if kernel == "decode_step" else f"gemv_{kernel}_3b_pmc.md"
@@ -67,6 +85,135 @@ def traffic_from_profiles(kernel):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def lin_params(c):
+    H, F = c["hidden_size"], c["intermediate_size"]
+    qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
+    return (qd + 2 * kd) * H + H * qd + 2 * F * H + H * F
+
+
+def prefill_flops(c, T):
+    """Linear layers for T tokens, lm_head for the last one, causal attention."""
+    L, V, H = c["num_hidden_layers"], c["vocab_size"], c["hidden_size"]
+    return (2 * T * L * lin_params(c) + 2 * V * H
+            + L * 4 * c["num_attention_heads"] * 128 * T * (T + 1) // 2)
+
+
+def run_cfg(args, engine, c):
+    import numpy as np
+    rng = np.random.default_rng(args.seed + 3)
+    cond = rng.integers(0, c["vocab_size"], size=512).tolist()
+    uncond = rng.integers(0, c["vocab_size"], size=512).tolist()
+    sampling = dict(temperature=1.0, top_p=0.93, top_k=50, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=1024)
+    engine.generate_tokens(cond, dict(sampling, max_tokens=16), args.seed, negative=uncond,
+                           cfg_scale=1.5)  # warm: graphs, code objects
+    tokens, timing, _ = engine.generate_tokens(cond, sampling, args.seed, negative=uncond,
+                                               cfg_scale=1.5)
+    decode_s = timing["seconds"] - timing["prefill_seconds"]
+    tps = (len(tokens) - 1) / decode_s
+    L = 512 + len(tokens) / 2  # mean per-branch KV length
+    step_bytes = weight_bytes(c) + 2 * L * KV_BYTES_PER_POS
+    log(f"[bench] cfg: {len(tokens)} tokens, prefill {timing['prefill_seconds']:.3f}s, "
+        f"decode {tps:.1f} tok/s")
+    return {"metric": "CFG decode tokens/sec (batch 2 cond+uncond, scale 1.5, top-k 50 / "
+                      "top-p 0.93, T 1.0)",
+            "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "3B decoder, CFG pair, 512 + 512 prompt ids, 1024 tokens",
+                       "driver": "yuear_generate_tokens (host loop, pipelined)"},
+            "prefill_seconds": round(timing["prefill_seconds"], 4),
+            "step_roofline": {"bytes_per_step": int(step_bytes),
+                              "frac": round(step_bytes * tps / PEAK_HBM, 4)},
+            "tokens": len(tokens)}
+
+
+def run_long(args, engine, c):
+    import numpy as np
+    import torch
+    T, end = 3000, 8192
+    rng = np.random.default_rng(args.seed + 4)
+    s = engine.session(1, end + 8)
+    warm = engine.session(1, 2048 + 8)
+    warm.prefill(0, rng.integers(0, c["vocab_size"], size=2048).tolist())  # code objects
+    warm.close()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    s.prefill(0, rng.integers(0, c["vocab_size"], size=T).tolist())
+    torch.cuda.synchronize()
+    pre_s = time.perf_counter() - t
+    flops = prefill_flops(c, T)
+    log(f"[bench] long: prefill {T} tokens {pre_s * 1e3:.1f} ms, "
+        f"{flops / pre_s / 1e12:.1f} TFLOP/s")
+    greedy = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                  penalty_window=50, min_tokens=0, max_tokens=end)
+    curve, reset = [], True
+    while s.position(0) + 512 <= end:
+        L0 = s.position(0)
+        ms, _ = s.time_generate(greedy, args.seed, 512, reset=reset)
+        reset = False
+        curve.append({"kv_from": L0 + 1, "kv_to": L0 + 512, "ms_per_token": round(ms, 4),
+                      "tokens_per_s": round(1e3 / ms, 1)})
+        log(f"[bench] long: KV {L0 + 1}-{L0 + 512}: {ms:.4f} ms/token")
+    return {"metric": "prefill TFLOP/s (3000 tokens) and decode ms/token vs KV length",
+            "value": round(flops / pre_s / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "3B decoder, 3000-token prefill then decode to KV 8192"},
+            "prefill_ms": round(pre_s * 1e3, 2), "prefill_flops": flops,
+            "mfma_frac": round(flops / pre_s / PEAK_BF16, 4), "decode_curve": curve}
+
+
+def run_batch8(args, engine, c):
+    import numpy as np
+    import torch
+    B, steps, cap = 8, 512, 6144
+    rng = np.random.default_rng(args.seed + 5)
+    lens = rng.integers(128, 2049, size=B)
+    s = engine.session(B, cap)
+    for b, n in enumerate(lens):
+        s.prefill(b, rng.integers(0, c["vocab_size"], size=int(n)).tolist())
+    greedy = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                  penalty_window=50, min_tokens=0, max_tokens=steps + 16)
+    s.time_generate(greedy, args.seed, 8, reset=True)  # warm (captures the graph)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    dev_ms, _ = s.time_generate(greedy, args.seed, steps, reset=False)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t
+    agg = B * steps / wall
+    mean_kv = float(np.mean(lens)) + 8 + steps / 2
+    step_bytes = weight_bytes(c) + B * mean_kv * KV_BYTES_PER_POS
+    # per-kernel device time at batch 8; the projections run on MFMA
+    # (v_mfma_f32_16x16x32_bf16, 8 of 16 columns live), so their MFMA
+    # utilisation is the useful flops over the dense bf16 peak
+    kernels = {}
+    pos = [s.position(b) for b in range(B)]
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head"):
+        ms = s.time_kernel(name, 56 if name != "lm_head" else 8)
+        if name == "attention":
+            nbytes = sum(kernel_bytes(c, name, p + 1) for p in pos)
+            flops = None
+        else:
+            n, k = gemv_shape(c, name)
+            nbytes = kernel_bytes(c, name, 0) + (B - 1) * (kernel_bytes(c, name, 0) - 2 * n * k)
+            flops = 2 * B * n * k
+        kernels[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes),
+                         "GBps": round(nbytes / (ms / 1e3) / 1e9, 1)}
+        if flops:
+            kernels[name]["mfma_util"] = round(flops / (ms / 1e3) / PEAK_BF16, 5)
+        log(f"[bench] batch8 {name:9s} {ms * 1e3:8.2f} us  {nbytes / 1e6:8.2f} MB  "
+            f"{nbytes / (ms / 1e3) / 1e9:7.1f} GB/s")
+    log(f"[bench] batch8: {agg:.1f} tok/s aggregate ({wall / steps * 1e3:.3f} ms/step)")
+    return {"metric": "aggregate decode tokens/sec, 8 independent sequences",
+            "value": round(agg, 2), "unit": "tokens/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "3B decoder, batch 8, prompts U[128,2048], capacity 6144, "
+                                   "512 greedy steps", "prompt_lengths": [int(x) for x in lens]},
+            "ms_per_step": round(wall / steps * 1e3, 4),
+            "step_roofline": {"bytes_per_step": int(step_bytes),
+                              "frac": round(step_bytes / (wall / steps) / PEAK_HBM, 4)},
+            "kernels": kernels}
 
 
 PHASES = ("qkv", "attention", "merge", "o_proj", "gate_up", "down")
@@ -120,6 +267,8 @@ def main():
     ap.add_argument("--kernel-launches", type=int, default=112)
     ap.add_argument("--decode", choices=("persistent", "kernels"), default="kernels",
                     help="decode step as one persistent kernel or one kernel per op")
+    ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8"), default="decode",
+                    help="workload (decode: the headline batch-1 KV-4096 line)")
     ap.add_argument("--phase-trace", action="store_true",
                     help="profiling mode: per-phase timeline of one persistent decode step")
     ap.add_argument("--kernel-only", default=None,
@@ -153,6 +302,12 @@ def main():
     weights = yuear.random_weights(c, args.seed)
     log(f"[bench] weights ready {time.perf_counter() - t_start:.1f}s; uploading")
     engine = yuear.Engine(c, weights)
+    if args.config != "decode":
+        line = {"cfg": run_cfg, "long": run_long, "batch8": run_batch8}[args.config](
+            args, engine, c)
+        print(json.dumps(line), flush=True)
+        log(f"[bench] total {time.perf_counter() - t_start:.1f}s")
+        return
     W, K = args.warmup, args.steps
     prefill = args.kv - 1 - W - (K - 1) // 2  # timed steps centred on KV length kv
     step_launches = 16

@@ -189,7 +189,10 @@ yuear_status yuear_session_time_steps(yuear_session *session, int32_t steps,
  * graph replays of (sampler -> decode step) with no host synchronisation in
  * between, timed with hipEvents on the session stream. The sampler state
  * (step counter, history) restarts when reset != 0. tokens_out (nullable)
- * receives the emitted native ids of this call. */
+ * receives the emitted native ids of this call (branch 0). With more than
+ * two branches every branch is an independent sequence (its own draw,
+ * history and seed + branch); with one or two, one draw feeds all branches
+ * (a request, or its CFG pair with cfg_scale 1). */
 yuear_status yuear_session_time_generate(yuear_session *session,
                                          const yuear_sampling *sampling,
                                          uint64_t seed, int32_t steps,

@@ -65,6 +65,33 @@ def assert_close_bf16(got_bits, ref_bits, rtol=2.0 ** -7, atol_frac=2.0 ** -9, s
     assert same >= exact_frac, f"only {same:.3f} bit-identical"
 
 
+def _f64(b):
+    import cpu_ref
+    return cpu_ref.bf16_to_f32(b).astype(np.float64)
+
+
+def fidelity_metrics(a, b):
+    d = _f64(a) - _f64(b)
+    cos = np.dot(_f64(a), _f64(b)) / (np.linalg.norm(_f64(a)) * np.linalg.norm(_f64(b)))
+    return {"max_abs": np.abs(d).max(), "rms": np.sqrt(np.mean(d * d)), "cos": cos}
+
+
+def check_fidelity(gpu, oracle32, oracle64):
+    """The reference's fidelity rule for multi-layer bf16 models
+    (tools/limits.py:21-79, tools/fidelity.py:124-148): the GPU's distance to
+    the fp64-accumulation oracle stays within twice the distance of the
+    fp32-accumulation oracle to it (max_abs, rms, 1 - cosine), and the argmax
+    agrees unless the top two are closer than that radius."""
+    radius = fidelity_metrics(oracle32, oracle64)
+    got = fidelity_metrics(gpu, oracle64)
+    print("oracle radius", radius, "gpu", got)
+    assert got["max_abs"] <= 2 * radius["max_abs"]
+    assert got["rms"] <= 2 * radius["rms"]
+    assert 1 - got["cos"] <= 2 * (1 - radius["cos"])
+    top = np.sort(_f64(oracle64))[-2:]
+    assert _f64(gpu).argmax() == _f64(oracle64).argmax() or top[1] - top[0] < 2 * radius["max_abs"]
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import cpu_ref

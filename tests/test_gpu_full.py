@@ -17,31 +17,9 @@ test_gpu_engine.py).
 import numpy as np
 import pytest
 
-from conftest import MODEL_3B
+from conftest import MODEL_3B, check_fidelity
 
 pytestmark = pytest.mark.gpu
-
-
-def f(b):
-    import cpu_ref
-    return cpu_ref.bf16_to_f32(b).astype(np.float64)
-
-
-def metrics(a, b):
-    d = f(a) - f(b)
-    cos = np.dot(f(a), f(b)) / (np.linalg.norm(f(a)) * np.linalg.norm(f(b)))
-    return {"max_abs": np.abs(d).max(), "rms": np.sqrt(np.mean(d * d)), "cos": cos}
-
-
-def check_fidelity(gpu, oracle32, oracle64):
-    radius = metrics(oracle32, oracle64)
-    got = metrics(gpu, oracle64)
-    print("oracle radius", radius, "gpu", got)
-    assert got["max_abs"] <= 2 * radius["max_abs"]
-    assert got["rms"] <= 2 * radius["rms"]
-    assert 1 - got["cos"] <= 2 * (1 - radius["cos"])
-    top = np.sort(f(oracle64))[-2:]
-    assert f(gpu).argmax() == f(oracle64).argmax() or top[1] - top[0] < 2 * radius["max_abs"]
 
 
 @pytest.fixture(scope="module")

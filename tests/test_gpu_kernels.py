@@ -56,6 +56,16 @@ GEMV_CASES = [  # (n, k, batch, norm, epilogue)
     (1024, 3072, 8, True, 0),     # batched sequences
     (1024, 8192, 8, False, 1),
     (1000, 256, 3, True, 0),      # ragged: odd batch, short rows, n % 8 != 0
+    # 3..8 rows: MFMA form (hidden 3072 and 2048 layer shapes)
+    (5120, 3072, 5, True, 0),
+    (3072, 3072, 4, False, 1),
+    (16384, 3072, 8, True, 2),
+    (3072, 8192, 6, False, 1),
+    (4096, 2048, 3, True, 0),
+    (12288, 2048, 7, True, 2),
+    (2048, 6144, 8, False, 1),
+    (1000, 3072, 3, True, 0),     # n % 16 != 0
+    (998, 3072, 5, True, 2),
     (96, 512, 1, False, 2),
 ]
 

@@ -315,7 +315,8 @@ struct yuear_session {
   float *scratch = nullptr, *alphas = nullptr;
   uint32_t *scratch_u = nullptr;
   int32_t *sstate = nullptr, *history = nullptr;
-  int history_cap = 0;
+  int history_cap = 0;       // history entries per branch set
+  int scratch_u_stride = 0;
   // prefill scratch
   int chunk = 0;
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
@@ -546,12 +547,16 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   HIPC(hipMemsetAsync(S.counters, 0, size_t(branches) * c.Hkv * 4, S.stream));
   int pow2 = 1;
   while (pow2 < S.phase.size) pow2 <<= 1;
-  S.scratch = S.alloc<float>(S.phase.size);
-  S.scratch_u = S.alloc<uint32_t>(size_t(S.phase.size) + 2 * size_t(pow2));
+  // sampler buffers: one set per branch when more than two branches sample
+  // independently (batched sequences), one shared set otherwise
+  const int sets = branches > 2 ? branches : 1;
+  S.scratch_u_stride = S.phase.size + 2 * pow2;
+  S.scratch = S.alloc<float>(size_t(S.phase.size) * sets);
+  S.scratch_u = S.alloc<uint32_t>(size_t(S.scratch_u_stride) * sets);
   S.alphas = S.alloc<float>(128);
-  S.sstate = S.alloc<int32_t>(2);
+  S.sstate = S.alloc<int32_t>(2 * sets);
   S.history_cap = kContext;
-  S.history = S.alloc<int32_t>(S.history_cap);
+  S.history = S.alloc<int32_t>(size_t(S.history_cap) * sets);
   S.chunk = std::min(capacity, 2048);
   const size_t T = S.chunk;
   S.px = S.alloc<uint16_t>(T * c.H);
@@ -995,6 +1000,12 @@ SamplerParams sampler_params(yuear_session &S, const yuear_sampling &s, uint64_t
   p.tokens_out = S.tok;
   p.scratch = S.scratch;
   p.scratch_u = S.scratch_u;
+  if (S.B > 2) {  // batched sequences: each branch is its own request
+    p.independent = 1;
+    p.history_stride = S.history_cap;
+    p.scratch_stride = S.phase.size;
+    p.scratch_u_stride = S.scratch_u_stride;
+  }
   return p;
 }
 
@@ -1104,6 +1115,9 @@ yuear_status yuear_session_sample(yuear_session *S, const yuear_sampling *sampli
       invalid("session, sampling and output are required");
     validate_sampling(*sampling);
     check_sampler_phase(*S, cfg_scale);
+    if (S->B > 2)
+      invalid("sessions of more than two branches sample each branch independently "
+              "(yuear_session_time_generate); sample one token per request session");
     if (seed >= (uint64_t(1) << 63))
       invalid("seed must be an integer in [0, 2**63)");
     if (history_len < 0 || history_len > S->history_cap || (history_len && !history))
@@ -1331,12 +1345,13 @@ yuear_status yuear_session_time_generate(yuear_session *S, const yuear_sampling 
       S->gen_key = key;
       reset = 1;
     }
-    int32_t st0[2] = {0, 0};
-    if (!reset) {
-      HIPC(hipMemcpy(st0, S->sstate, 8, hipMemcpyDeviceToHost));
-    } else {
-      HIPC(hipMemcpy(S->sstate, st0, 8, hipMemcpyHostToDevice));
-    }
+    const int sets = S->B > 2 ? S->B : 1;
+    std::vector<int32_t> st(2 * sets, 0);
+    if (!reset)
+      HIPC(hipMemcpy(st.data(), S->sstate, st.size() * 4, hipMemcpyDeviceToHost));
+    else
+      HIPC(hipMemcpy(S->sstate, st.data(), st.size() * 4, hipMemcpyHostToDevice));
+    const int32_t st0[2] = {st[0], st[1]};
     const int first = st0[0];
     if (first + steps > S->history_cap)
       invalid("generation history exceeds the context");

@@ -254,6 +254,8 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t s) {
   if (p.k % 8 || p.k > 8192 || p.n < 1 || p.batch < 1 || p.batch > 8 ||
       (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2))
     return hipErrorInvalidValue;
+  if (gemv_mfma_supported(p))  // 3..8 rows: MFMA (gemv_mfma.hip)
+    return launch_gemv_mfma(p, s);
   // Rows per wave: 2 keeps ~12 KiB of weight loads in flight per wave at
   // K = 3072; the SwiGLU epilogue needs an even count; K = 8192 uses 1 row.
   const bool wide = p.k > 4096;

@@ -1,0 +1,236 @@
+// Batched decode projections (3..8 independent rows) on MFMA, gfx950.
+//
+// y[b, r] = x[b, :] . W[row(r), :] with fp32 accumulation and one bf16
+// rounding (native/src/ar.cpp:20-29), for the batched-sequence decode where
+// a VALU GEMV would do 8 dot products per weight element. The weight stream
+// is still read exactly once: the work is HBM-bound, v_mfma_f32_16x16x32_bf16
+// only keeps the arithmetic off the VALU.
+//
+// Workgroup: 16 consecutive weight rows; its WAVES waves split K, wave w
+// owning k in [w KW, (w + 1) KW), KW = KSTEPS * 32. MFMA operands per k-step
+// (layouts of the 16x16x32 bf16 form): A = 16 weight rows x 32 k, lane l
+// holding row l % 16, k 8 (l / 16) + [0, 8) (one 16-byte load); B = 32 k x
+// 16 batch columns, lane l holding column l % 16 (zero beyond the batch)
+// from the staged activations; D = 16 rows x 16 columns, lane l holding
+// column l % 16, rows 4 (l / 16) + [0, 4).
+//
+// Order: the activation loads are issued first, then all KSTEPS weight loads
+// of the wave (non-temporal), so the activation staging waits only for the
+// former (the vector-memory counter drains in issue order). Activations are
+// staged in LDS with rows padded by 16 bytes (conflict-free 16-byte reads
+// across the 16 batch columns), gathered from the embedding for layer 0 and
+// RMS-normalised in place when a gain is given (ar.cpp:30-35 rounding
+// points). The waves' D tiles are summed through LDS in wave order, then the
+// epilogue (store / residual / SwiGLU) runs one thread per (row, column).
+#include "common.h"
+#include "kernels.h"
+
+namespace yuear {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+template <int WAVES, int KSTEPS, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvParams p) {
+  extern __shared__ u32x4 lds[];
+  constexpr int NT = WAVES * 64;
+  constexpr int K = WAVES * KSTEPS * 32;
+  constexpr int NCH = K / 8;           // 16-byte chunks per activation row
+  constexpr int ROWC = NCH + 1;        // staged row stride (chunks): +16 bytes of padding
+  constexpr int XPT = (8 * NCH + NT - 1) / NT;
+  __shared__ float red_ss[8][WAVES];
+  __shared__ float scale_b[8];
+  float *red = reinterpret_cast<float *>(lds + 8 * ROWC);  // [WAVES][16][16]
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int B = p.batch;
+  const int n0 = blockIdx.x * 16;
+
+  // 1. activation loads (branch-free: clamped, masked later)
+  u32x4 xr[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int idx = min(int(threadIdx.x) + NT * i, B * NCH - 1);
+    const int b = idx / NCH, c = idx - b * NCH;
+    const uint16_t *src;
+    if (p.embed) {
+      const int t = min(max(p.tokens[b], 0), p.embed_rows - 1);
+      src = p.embed + size_t(t) * K;
+    } else {
+      src = p.x + size_t(b) * p.x_stride;
+    }
+    xr[i] = reinterpret_cast<const u32x4 *>(src)[c];
+  }
+
+  // 2. this wave's weight stream: row n0 + l % 16 (clamped; mapped for the
+  // lm_head phases), k = wave * KW + 32 s + 8 (l / 16)
+  u32x4 a[KSTEPS];
+  {
+    const int lr = min(n0 + (lane & 15), p.n - 1);
+    const int row = lr < p.seg0_len ? p.seg0_start + lr : p.seg1_start + (lr - p.seg0_len);
+    const u32x4 *w =
+        reinterpret_cast<const u32x4 *>(p.w + size_t(row) * K) + wave * (KSTEPS * 4) + (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      a[s] = __builtin_nontemporal_load(w + 4 * s);
+  }
+
+  // 3. stage (and gather-copy) the activations, RMSNorm
+  float ss[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+    ss[b] = 0.f;
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int idx = int(threadIdx.x) + NT * i;
+    if (idx < B * NCH) {
+      const int b = idx / NCH, c = idx - b * NCH;
+      const u32x4 v = xr[i];
+      lds[b * ROWC + c] = v;
+      if (p.x_out && blockIdx.x == 0)
+        reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v;
+      if (p.norm_w) {
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = bflo(w4[q]), hi = bfhi(w4[q]);
+          t += lo * lo;
+          t += hi * hi;
+        }
+#pragma unroll
+        for (int bb = 0; bb < 8; ++bb)
+          ss[bb] += bb == b ? t : 0.f;
+      }
+    }
+  }
+  if (p.norm_w) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const float t = wave_sum(ss[b]);
+      if (lane == 0)
+        red_ss[b][wave] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+      float total = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w)
+        total += red_ss[threadIdx.x][w];
+      scale_b[threadIdx.x] = rbf(1.0f / __builtin_sqrtf(total / float(K) + p.eps));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int idx = int(threadIdx.x) + NT * i;
+      if (idx < B * NCH) {
+        const int b = idx / NCH, c = idx - b * NCH;
+        const float scale = scale_b[b];
+        const u32x4 v = lds[b * ROWC + c], g = reinterpret_cast<const u32x4 *>(p.norm_w)[c];
+        const uint32_t vi[4] = {v.x, v.y, v.z, v.w}, gi[4] = {g.x, g.y, g.z, g.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = f2bf(rbf(bflo(vi[q]) * scale) * bflo(gi[q]));
+          const uint32_t hi = f2bf(rbf(bfhi(vi[q]) * scale) * bfhi(gi[q]));
+          o[q] = lo | (hi << 16);
+        }
+        lds[b * ROWC + c] = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+  __syncthreads();
+
+  // 4. MFMA over this wave's K slice
+  const int col = lane & 15;
+  const bool live = col < B;
+  const u32x4 *xrow = lds + min(col, B - 1) * ROWC + wave * (KSTEPS * 4) + (lane >> 4);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    const u32x4 bv = live ? xrow[4 * s] : u32x4{0u, 0u, 0u, 0u};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[s]), as_bf16x8(bv), acc, 0, 0, 0);
+  }
+
+  // 5. sum the waves' tiles (wave order), epilogue per (row, column)
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    red[(wave * 16 + 4 * (lane >> 4) + t) * 16 + col] = acc[t];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;  // row n0 + i, column j
+    float y = 0.f, y1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      y += red[(w * 16 + i) * 16 + j];
+      if constexpr (EPI == kEpiSwiGLU)
+        y1 += red[(w * 16 + (i | 1)) * 16 + j];
+    }
+    const int row = n0 + i;
+    if (j < B && row < p.n) {
+      uint16_t *yb = p.y + size_t(j) * p.y_stride;
+      if constexpr (EPI == kEpiSwiGLU) {
+        if ((i & 1) == 0) {  // rows (2m, 2m + 1) = (gate_m, up_m)
+          const float g = rbf(y), u = rbf(y1);
+          const float act = rbf(g * (1.0f / (1.0f + expf(-g))));
+          yb[row >> 1] = f2bf(act * u);
+        }
+      } else if constexpr (EPI == kEpiResidual) {
+        yb[row] = f2bf(bf2f(yb[row]) + rbf(y));
+      } else {
+        yb[row] = f2bf(y);
+      }
+    }
+  }
+  if (p.advance && blockIdx.x == 0 && threadIdx.x < p.batch)
+    p.advance[threadIdx.x] += 1;
+}
+
+template <int WAVES, int KSTEPS, int EPI>
+hipError_t launch_wke(const GemvParams &p, hipStream_t s) {
+  constexpr int K = WAVES * KSTEPS * 32;
+  const size_t lds = size_t(8) * (K / 8 + 1) * 16 + size_t(WAVES) * 256 * 4;
+  auto kern = gemv_mfma_kernel<WAVES, KSTEPS, EPI>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  if (e != hipSuccess)
+    return e;
+  hipLaunchKernelGGL(kern, dim3((p.n + 15) / 16), dim3(WAVES * 64), lds, s, p);
+  return hipGetLastError();
+}
+
+template <int WAVES, int KSTEPS>
+hipError_t launch_wk(const GemvParams &p, hipStream_t s) {
+  switch (p.epilogue) {
+  case kEpiStore: return launch_wke<WAVES, KSTEPS, kEpiStore>(p, s);
+  case kEpiResidual: return launch_wke<WAVES, KSTEPS, kEpiResidual>(p, s);
+  case kEpiSwiGLU: return launch_wke<WAVES, KSTEPS, kEpiSwiGLU>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool gemv_mfma_supported(const GemvParams &p) {
+  return p.batch >= 3 && p.batch <= 8 && (p.x_stride % 8 == 0 || p.embed) &&
+         (p.k == 3072 || p.k == 8192 || p.k == 2048 || p.k == 6144) &&
+         (p.epilogue != kEpiSwiGLU || p.n % 2 == 0);
+}
+
+hipError_t launch_gemv_mfma(const GemvParams &p, hipStream_t s) {
+  if (!gemv_mfma_supported(p) || p.n < 1)
+    return hipErrorInvalidValue;
+  switch (p.k) {
+  case 3072: return launch_wk<4, 24>(p, s);   // 4 waves x 768 k
+  case 8192: return launch_wk<16, 16>(p, s);  // 16 waves x 512 k
+  case 2048: return launch_wk<4, 16>(p, s);
+  case 6144: return launch_wk<16, 12>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace yuear

@@ -33,6 +33,10 @@ struct GemvParams {
   int32_t *advance = nullptr;  // block 0 increments advance[0..batch)
 };
 hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
+// MFMA form for 3..8 independent rows (batched sequences); launch_gemv
+// dispatches to it when gemv_mfma_supported(p).
+bool gemv_mfma_supported(const GemvParams &p);
+hipError_t launch_gemv_mfma(const GemvParams &p, hipStream_t s);
 
 // Split-K flash-decode attention for one layer, all branches, with the
 // q/k RMSNorm + RoPE prologue, the KV append of the current token and the
@@ -78,6 +82,13 @@ struct SamplerParams {
   int32_t *tokens_out = nullptr;  // [branches] next input token (native)
   float *scratch = nullptr;       // [n] fp32 scores
   uint32_t *scratch_u = nullptr;  // [2 * n] survivor keys / indices
+  // Independent branches (batched sequences): workgroup b samples branch b
+  // from its own logits row with its own state[2b..2b+1], history row
+  // (history + b * history_stride), scratch (+ b * scratch_stride /
+  // scratch_u_stride) and seed + b; no CFG. Otherwise one draw is shared by
+  // all branches (a request, or a CFG pair).
+  int independent = 0;
+  int history_stride = 0, scratch_stride = 0, scratch_u_stride = 0;
 };
 hipError_t launch_sampler(const SamplerParams &p, hipStream_t s);
 

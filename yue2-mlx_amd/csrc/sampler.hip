@@ -193,8 +193,20 @@ __device__ __forceinline__ bool special(const Shared &sh, int i) {
   return (sh.u.bits[i >> 5] >> (i & 31)) & 1u;
 }
 
-__global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
+__global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
   __shared__ Shared sh;
+  SamplerParams p = p0;
+  if (p0.independent) {  // workgroup b: branch b on its own, as a 1-branch request
+    const int b = blockIdx.x;
+    p.logits += size_t(b) * p0.ls;
+    p.branches = 1;
+    p.state += 2 * b;
+    p.history += size_t(b) * p0.history_stride;
+    p.tokens_out += b;
+    p.scratch += size_t(b) * p0.scratch_stride;
+    p.scratch_u += size_t(b) * p0.scratch_u_stride;
+    p.seed += uint64_t(b);
+  }
   const int tid = threadIdx.x;
   const int n = p.n;
   if (p.state[1])
@@ -468,9 +480,11 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p) {
 hipError_t launch_sampler(const SamplerParams &p, hipStream_t s) {
   if (p.n < 1 || p.n > 64 * kSortLds || p.ls < p.n || p.ls % 8 || p.branches < 1 ||
       p.branches > 8 || p.penalty_window > 128 || !p.scratch || !p.scratch_u || !p.state ||
-      !p.tokens_out)
+      !p.tokens_out ||
+      (p.independent && (p.history_stride < p.max_tokens || p.scratch_stride < p.n ||
+                         p.scratch_u_stride < p.n)))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sampler_kernel, dim3(1), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(sampler_kernel, dim3(p.independent ? p.branches : 1), dim3(kT), 0, s, p);
   return hipGetLastError();
 }
 
