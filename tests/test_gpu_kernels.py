@@ -113,7 +113,7 @@ def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_hea
                                          splits):
     rng = np.random.default_rng(sum(batch_pos) + heads + splits)
     B = len(batch_pos)
-    cap = max(batch_pos) + 9
+    cap = yuear_lib.kv_slots(max(batch_pos) + 9)  # V cache: whole 32-slot blocks
     qkvw = (heads + 2 * kv_heads) * 128
     qkv = bf(rng.normal(size=(B, qkvw)))
     cache_k = bf(rng.normal(size=(B, kv_heads, cap, 128)))
@@ -131,7 +131,8 @@ def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_hea
         refs.append(oracle.attention(q[None], K, V, pos)[0])
         kref.append(k)
         vref.append(v)
-    args = [dev(torch, a) for a in (qkv, qn, kn, cos, sin, cache_k, cache_v)]
+    args = [dev(torch, a) for a in (qkv, qn, kn, cos, sin, cache_k,
+                                    yuear_lib.v_blocked(cache_v))]
     dpos = dev(torch, np.array(batch_pos, np.int32))
     out = dev(torch, np.zeros((B, heads * 128), np.uint16))
     rc = yuear_lib.lib.yuear_op_attention_decode(
@@ -142,19 +143,20 @@ def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_hea
     got = host(torch, out)
     ref = np.stack(refs)
     assert_close_bf16(got, ref, exact_frac=0.8)
-    gk, gv = host(torch, args[5]), host(torch, args[6])
+    gk, gv = host(torch, args[5]), yuear_lib.v_unblocked(host(torch, args[6]))
     for b, pos in enumerate(batch_pos):
         np.testing.assert_array_equal(gv[b][:, pos], vref[b])
         assert ulps_bf16(gk[b][:, pos], kref[b]).max() <= 1
         others = np.ones(cap, bool)
         others[pos] = False
         np.testing.assert_array_equal(gk[b][:, others], cache_k[b][:, others])
+        np.testing.assert_array_equal(gv[b][:, others], cache_v[b][:, others])
 
 
 def test_attention_decode_ignores_unused_slots(torch, yuear_lib):
     # vendor test_cuda_graph.py:62-79: slots beyond the position are invisible
     rng = np.random.default_rng(9)
-    heads, kv, pos, cap = 24, 8, 300, 400
+    heads, kv, pos, cap = 24, 8, 300, 416
     qkv = bf(rng.normal(size=(1, (heads + 2 * kv) * 128)))
     k = bf(rng.normal(size=(1, kv, cap, 128)))
     v = bf(rng.normal(size=(1, kv, cap, 128)))
@@ -165,7 +167,7 @@ def test_attention_decode_ignores_unused_slots(torch, yuear_lib):
         if poison:
             kk[..., pos + 1:, :] = bf(1000.0)
             vv[..., pos + 1:, :] = bf(-1000.0)
-        a = [dev(torch, t) for t in (qkv, cos, sin, kk, vv)]
+        a = [dev(torch, t) for t in (qkv, cos, sin, kk, yuear_lib.v_blocked(vv))]
         dpos = dev(torch, np.array([pos], np.int32))
         out = dev(torch, np.zeros((1, heads * 128), np.uint16))
         assert yuear_lib.lib.yuear_op_attention_decode(
@@ -198,12 +200,12 @@ def test_gemm_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual):
                                                    (65, 10, 24, 8), (200, 333, 16, 8)])
 def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, heads, kv_heads):
     rng = np.random.default_rng(T + pos0)
-    cap = pos0 + T + 3
+    cap = yuear_lib.kv_slots(pos0 + T + 3)
     q = bf(rng.normal(size=(T, heads, 128)))
     kc = bf(rng.normal(size=(kv_heads, cap, 128)))
     vc = bf(rng.normal(size=(kv_heads, cap, 128)))
     ref = oracle.attention(q, kc, vc, pos0)
-    a = [dev(torch, t) for t in (q, kc, vc)]
+    a = [dev(torch, t) for t in (q, kc, yuear_lib.v_blocked(vc))]
     out = dev(torch, np.zeros((T, heads * 128), np.uint16))
     assert yuear_lib.lib.yuear_op_attention_prefill(a[0].data_ptr(), a[1].data_ptr(),
                                                     a[2].data_ptr(), T, pos0, heads, kv_heads,

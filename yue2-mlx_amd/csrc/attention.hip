@@ -4,13 +4,15 @@
 // SDPA with fp32 softmax/accumulation, bf16 output) and ar.cpp:88-91.
 //
 // Grid (max_splits, Hkv, batch), 256 threads. Workgroup (s, h, b) owns keys
-// [s*chunk, min(L, (s+1)*chunk)) of kv head h of branch b, L = pos[b] + 1, and
+// [s*chunk, min(L, (s+1)*chunk)) of kv head h of branch b, L = pos[b] + 1
+// (chunk a multiple of the 32-key V block), and
 // all G = Hq/Hkv query heads sharing that kv head, so each K/V byte is read
 // from HBM exactly once per step. The chunk length is derived on device from
 // pos[b], so one captured graph serves every KV length up to capacity.
 //
-// The per-split math (prologue, passes, online softmax, wave combine) is
-// attn_core.h, shared with the persistent step. Here: the q/k/v inputs are
+// The per-split math (prologue, MFMA passes, online softmax, wave combine) is
+// attn_core.h, shared with the persistent step; it also fixes the cache
+// layout (K row-major, V in dim-major 32-key blocks). Here: the q/k/v inputs are
 // issued first, then the split's first 128-key pass of K/V, so the prologue
 // (q/k RMSNorm + RoPE) overlaps the K/V stream; the workgroup whose range
 // contains slot pos[b] appends the new K/V. Partials (m, l, o) go to a
@@ -53,16 +55,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
     return;  // uniform for the grid slice of this branch: nothing to append
   const int L = pos + 1;
   const int per = (L + p.max_splits - 1) / p.max_splits;
-  const int chunk = (per + 15) & ~15;
+  const int chunk = (per + attn::kBlock - 1) & ~(attn::kBlock - 1);
   const int s0 = s * chunk, s1 = min(L, s0 + chunk);
   const bool active = s0 < s1;
-  const size_t head_base = (size_t(b) * Hkv + kvh) * p.capacity;  // row index base
+  const size_t head_base = (size_t(b) * Hkv + kvh) * p.capacity;  // slot index base
   const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.k_cache) + head_base * (D / 8);
   const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.v_cache) + head_base * (D / 8);
   const size_t part = (size_t(b) * Hkv + kvh) * p.max_splits;
 
   if (active) {
-    const int grp = lane >> 4, sub = lane & 15;
     const int last_cached = pos > 0 ? pos - 1 : 0;
     // q/k/v inputs of this wave's heads (h = wave, wave + 4 < G + 2) first,
     // then the first pass of K/V: the prologue waits only for the former
@@ -75,9 +76,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
                                : size_t(p.heads + (h - G) * Hkv + kvh) * D;
       pair[j] = reinterpret_cast<const uint32_t *>(row + col)[lane];
     }
-    u32x4 kr[attn::kRows], vr[attn::kRows];
-    attn::load_k(kc, s0, wave, grp, sub, last_cached, kr);
-    attn::load_v(vc, s0, wave, grp, sub, last_cached, vr);
+    u32x4 kr[8], vr[8];
+    attn::load_k(kc, s0, wave, lane, last_cached, kr);
+    attn::load_v(vc, s0, wave, lane, last_cached, vr);
 
     // ---- prologue: q heads, current k, current v ----
     const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
@@ -88,18 +89,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
       const int h = wave + 4 * j;
       if (h < G + 2)
         attn::prologue_head<G>(sh, h, pair[j], h < G ? p.q_norm : p.k_norm, p.eps, cs, sn,
-                               qscale, lane);
+                               lane);
     }
     __syncthreads();
-    if (pos >= s0 && pos < s1 && threadIdx.x < 2 * (D / 8)) {  // append (ar.cpp:119-123)
-      const int which = threadIdx.x / (D / 8), c = threadIdx.x % (D / 8);
-      u32x4 *dst = reinterpret_cast<u32x4 *>(which ? p.v_cache : p.k_cache) +
-                   (head_base + pos) * (D / 8) + c;
-      *dst = sh.kv_new[which][c];
+    if (pos >= s0 && pos < s1 && threadIdx.x < D / 8 + D) {  // append (ar.cpp:119-123)
+      if (threadIdx.x < D / 8) {  // K row: 16 bytes per thread
+        reinterpret_cast<u32x4 *>(p.k_cache)[(head_base + pos) * (D / 8) + threadIdx.x] =
+            sh.kv_new[0][threadIdx.x];
+      } else {  // V: one dim per thread into its block column
+        const int d = threadIdx.x - D / 8;
+        p.v_cache[head_base * D + attn::v_index(pos, d)] =
+            reinterpret_cast<const uint16_t *>(&sh.kv_new[1][0])[d];
+      }
     }
 
     // ---- passes over the split, then the 4-wave combine ----
-    attn::split<G>(sh, kc, vc, s0, s1, pos, last_cached, lane, wave, kr, vr);
+    attn::split<G>(sh, kc, vc, s0, s1, pos, last_cached, lane, wave, qscale, kr, vr);
     __syncthreads();
     for (int e = threadIdx.x; e < G * D; e += 256) {
       float o, M, l;
@@ -192,7 +197,8 @@ hipError_t launch_g(const AttnDecodeParams &p, hipStream_t s) {
 
 hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s) {
   if (p.head_dim != D || p.kv_heads < 1 || p.heads % p.kv_heads || p.max_splits < 1 ||
-      p.max_splits > kMaxSplits || p.batch < 1 || p.capacity < 1)
+      p.max_splits > kMaxSplits || p.batch < 1 || p.capacity < 1 ||
+      p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   switch (p.heads / p.kv_heads) {
   case 1: return launch_g<1>(p, s);

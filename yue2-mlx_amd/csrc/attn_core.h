@@ -1,16 +1,30 @@
-// Split-K decode attention core for head_dim 128 on gfx950, shared by the
-// per-op kernel (attention.hip) and the persistent step (decode.hip): both
-// call these functions, so the two decode paths compute the same bits.
+// Split-K decode attention core for head_dim 128 on gfx950 MFMA, shared by
+// the per-op kernel (attention.hip) and the persistent step (decode.hip):
+// both call these functions, so the two decode paths compute the same bits.
 //
 // Reference: native/src/ar.cpp:268-291 (q/k RMSNorm, RoPE, SDPA with fp32
 // softmax and accumulation) and ar.cpp:88-91.
 //
-// A workgroup (4 waves) owns keys [s0, s1) of one kv head and the G query
-// heads sharing it. A pass covers kPass = 128 keys: wave w takes keys
-// t0 + 32 w + [0, 32), its four 16-lane groups one key row each per step
-// (row i of group g is key t0 + 32 w + 4 i + g), each lane 8 of the 128
-// dims, so a wave-wide load is 1 KiB of 4 consecutive key rows. Scores and
-// the online softmax run in fp32 with log2(e) folded into q (exp2).
+// A workgroup (4 waves) owns keys [s0, s1) of one kv head and the G <= 16
+// query heads sharing it. A pass covers kPass = 128 keys: wave w takes the
+// 32-key block t0 + 32 w. Both products run on v_mfma_f32_16x16x32_bf16 with
+// the G heads as the 16 MFMA columns (columns >= G are zero):
+//
+//   S^T[key][head] = K[key][:] . q[head][:]   two 16-key tiles x 4 k-steps
+//   O^T[dim][head] += V^T[dim][key] . P^T[key][head]   8 dim tiles
+//
+// The rows of the two S^T tiles are permuted (row i of tile T is key
+// 8 (i / 4) + 4 T + i % 4 of the block) so that lane (head j, row group r)
+// ends up holding the scores of keys 8 r + [0, 8): exactly the B operand of
+// P.V, with no data movement between the products. P (fp32) is fed as the
+// sum of three bf16 pieces (hi, mid, lo: 24 significant bits, three MFMAs),
+// q and K are bf16 already, so every product is exact and every sum is fp32
+// like the reference's opmath.
+//
+// V cache layout (per branch and kv head): blocks of 32 keys, each stored
+// dim-major [128][32] (v_index below), so the A operand of P.V -- 8
+// consecutive keys of one dim per lane -- is one 16-byte load, and a wave's
+// load of a dim tile is 1 KiB contiguous. K stays row-major [slot][128].
 #pragma once
 #include "common.h"
 
@@ -18,44 +32,62 @@ namespace yuear {
 namespace attn {
 
 constexpr int D = 128;
-constexpr int kRows = 8;                  // key rows per lane group per pass
-constexpr int kPass = 4 * 4 * kRows;      // keys per workgroup pass
+constexpr int kBlock = 32;           // keys per V block = keys per wave per pass
+constexpr int kPass = 4 * kBlock;    // keys per workgroup pass
 constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Element (slot t, dim d) of one head's V cache, in elements.
+__host__ __device__ __forceinline__ size_t v_index(int t, int d) {
+  return size_t(t >> 5) * (kBlock * D) + size_t(d) * kBlock + (t & (kBlock - 1));
+}
 
 template <int G>
 struct Lds {
-  float q[G][D];            // normalised, rotated, scaled q (fp32)
+  u32x4 q[G][D / 8];        // normalised, rotated q heads (bf16, unscaled)
   u32x4 kv_new[2][D / 8];   // current key / value (bf16)
   float w_m[4][G], w_l[4][G];
   float w_o[4][G][D];
 };
 
-__device__ __forceinline__ int key_of(int t0, int wave, int i, int grp) {
-  return t0 + wave * (4 * kRows) + i * 4 + grp;
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ void unpack8(u32x4 v, float *f) {
-  f[0] = bflo(v.x); f[1] = bfhi(v.x);
-  f[2] = bflo(v.y); f[3] = bfhi(v.y);
-  f[4] = bflo(v.z); f[5] = bfhi(v.z);
-  f[6] = bflo(v.w); f[7] = bfhi(v.w);
+// Offset in its 32-key block of row i of S^T tile T.
+__device__ __forceinline__ int key_ofs(int T, int i) { return 8 * (i >> 2) + 4 * T + (i & 3); }
+
+// K rows of this wave's block starting at t0 + 32 wave (A operands of S^T):
+// kr[4 T + s] = key key_ofs(T, lane % 16), dims 32 s + 8 (lane / 16) + [0, 8).
+// Rows beyond the written part of the cache are clamped to last_cached
+// (their scores are masked; the current key comes from LDS).
+__device__ __forceinline__ void load_k(const u32x4 *kc, int t0, int wave, int lane,
+                                       int last_cached, u32x4 (&kr)[8]) {
+  const int r = lane >> 4, i = lane & 15;
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+    const int key = min(t0 + kBlock * wave + key_ofs(T, i), last_cached);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      kr[4 * T + s] = kc[size_t(key) * (D / 8) + 4 * s + r];
+  }
 }
 
-// Keys of a pass (all K rows first, then all V rows, so that the scores wait
-// only for K). Keys at or beyond the current slot come from LDS or are
-// masked; the clamp keeps every address inside the written part of the
-// cache (last_cached = max(pos - 1, 0)).
-__device__ __forceinline__ void load_k(const u32x4 *kc, int t0, int wave, int grp, int sub,
-                                       int last_cached, u32x4 (&kr)[kRows]) {
+// V^T of the same block (A operands of O^T): vr[dt] = dim 16 dt + lane % 16,
+// keys 8 (lane / 16) + [0, 8). A block past last_cached's block holds only
+// masked keys (and the current key, taken from LDS), so it is clamped.
+__device__ __forceinline__ void load_v(const u32x4 *vc, int t0, int wave, int lane,
+                                       int last_cached, u32x4 (&vr)[8]) {
+  const int r = lane >> 4, d = lane & 15;
+  const int blk = min((t0 >> 5) + wave, last_cached >> 5);
+  const u32x4 *base = vc + size_t(blk) * (kBlock * D / 8);
 #pragma unroll
-  for (int i = 0; i < kRows; ++i)
-    kr[i] = kc[size_t(min(key_of(t0, wave, i, grp), last_cached)) * (D / 8) + sub];
-}
-__device__ __forceinline__ void load_v(const u32x4 *vc, int t0, int wave, int grp, int sub,
-                                       int last_cached, u32x4 (&vr)[kRows]) {
-#pragma unroll
-  for (int i = 0; i < kRows; ++i)
-    vr[i] = vc[size_t(min(key_of(t0, wave, i, grp), last_cached)) * (D / 8) + sub];
+  for (int dt = 0; dt < 8; ++dt)
+    vr[dt] = base[(16 * dt + d) * (kBlock / 8) + r];
 }
 
 // Prologue for head h of the workgroup (h < G: query head, h == G: key,
@@ -64,127 +96,143 @@ __device__ __forceinline__ void load_v(const u32x4 *vc, int t0, int wave, int gr
 template <int G, class GainPtr>
 __device__ __forceinline__ void prologue_head(Lds<G> &sh, int h, uint32_t pair, GainPtr gain,
                                               float eps, const uint16_t *cs, const uint16_t *sn,
-                                              float qscale, int lane) {
+                                              int lane) {
   float y0 = bflo(pair), y1 = bfhi(pair);
   if (h <= G)
     norm_rope_head(y0, y1, gain, eps, cs, sn, lane, y0, y1);
-  if (h < G) {
-    sh.q[h][2 * lane] = y0 * qscale;
-    sh.q[h][2 * lane + 1] = y1 * qscale;
-  } else {
-    reinterpret_cast<uint32_t *>(&sh.kv_new[h - G][0])[lane] =
-        uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
-  }
+  const uint32_t packed = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
+  if (h < G)
+    reinterpret_cast<uint32_t *>(&sh.q[h][0])[lane] = packed;
+  else
+    reinterpret_cast<uint32_t *>(&sh.kv_new[h - G][0])[lane] = packed;
+}
+
+// bf16 element e of a 16-byte vector replaced by `val`.
+__device__ __forceinline__ u32x4 with_elem(u32x4 v, int e, uint32_t val) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    if (q == (e >> 1))
+      w[q] = (e & 1) ? (w[q] & 0xffffu) | (val << 16) : (w[q] & 0xffff0000u) | val;
+  return u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // One pass over keys [t0, t0 + kPass) ∩ [s0, s1) with the online softmax
-// state of this lane (m, l per head; o: 8 dims per head). kr / vr hold the
-// pass's rows on entry; when `more`, the next pass's K rows are issued into
-// kr as soon as the scores are formed, and its V rows into vr after P.V.
+// state of this lane (head lane % 16): m, l (over this lane's keys), o (O^T
+// tiles: dims 16 dt + 4 (lane / 16) + [0, 4)). kr / vr hold the pass's
+// operands on entry; when `more`, the next pass's K rows are issued into kr
+// right after the S^T products and its V^T rows into vr after P.V.
 template <int G>
 __device__ __forceinline__ void pass(const Lds<G> &sh, const u32x4 *kc, const u32x4 *vc, int t0,
                                      int s1, int pos, int last_cached, bool more, int wave,
-                                     int grp, int sub, u32x4 (&kr)[kRows], u32x4 (&vr)[kRows],
-                                     float (&m_run)[G], float (&l_run)[G], float (&o_run)[G][8]) {
-  float sc[kRows][G];
+                                     int lane, const u32x4 (&qb)[4], float qscale,
+                                     u32x4 (&kr)[8], u32x4 (&vr)[8], float &m_run, float &l_run,
+                                     f32x4 (&o)[8]) {
+  const int r = lane >> 4, i = lane & 15;
+  const int blk0 = t0 + kBlock * wave;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    const int key = key_of(t0, wave, i, grp);
-    if (key == pos)
-      kr[i] = sh.kv_new[0][sub];
-    float kf[8];
-    unpack8(kr[i], kf);
+  for (int T = 0; T < 2; ++T)
+    if (blk0 + key_ofs(T, i) == pos) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float *q = &sh.q[h][sub * 8];  // LDS broadcast within a lane group
-      float acc = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        acc = fmaf(q[e], kf[e], acc);
-      acc = row_sum16(acc);  // the 16 lanes of this key row
-      sc[i][h] = key < s1 ? acc : -__builtin_inff();
+      for (int s = 0; s < 4; ++s)
+        kr[4 * T + s] = sh.kv_new[0][4 * s + r];
     }
+  f32x4 st[2];
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+    st[T] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      st[T] = mfma(kr[4 * T + s], qb[s], st[T]);
   }
   if (more)
-    load_k(kc, t0 + kPass, wave, grp, sub, last_cached, kr);
+    load_k(kc, t0 + kPass, wave, lane, last_cached, kr);
+  // the current key's values (dim 16 dt + i) into element pos - (blk0 + 8 r)
+  const int ep = pos - (blk0 + 8 * r);
+  if (ep >= 0 && ep < 8) {
+    const uint16_t *vn = reinterpret_cast<const uint16_t *>(&sh.kv_new[1][0]);
 #pragma unroll
-  for (int i = 0; i < kRows; ++i)
-    if (key_of(t0, wave, i, grp) == pos)
-      vr[i] = sh.kv_new[1][sub];
+    for (int dt = 0; dt < 8; ++dt)
+      vr[dt] = with_elem(vr[dt], ep, vn[16 * dt + i]);
+  }
+  // scores of keys blk0 + 8 r + e, e = 4 T + t
+  float sc[8];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float mx = sc[0][h];
+  for (int T = 0; T < 2; ++T)
 #pragma unroll
-    for (int i = 1; i < kRows; ++i)
-      mx = fmaxf(mx, sc[i][h]);
-    mx = max_halves(max_row_pairs(mx));  // over the 4 lane groups
-    const float m_new = fmaxf(m_run[h], mx);
-    if (m_new == -__builtin_inff())
-      continue;  // nothing visible yet in this wave
-    const float corr = __builtin_amdgcn_exp2f(m_run[h] - m_new);
-    float lsum = 0.f;
-    float pw[kRows];
+    for (int t = 0; t < 4; ++t)
+      sc[4 * T + t] = blk0 + 8 * r + 4 * T + t < s1 ? st[T][t] * qscale : -__builtin_inff();
+  float mx = sc[0];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      pw[i] = __builtin_amdgcn_exp2f(sc[i][h] - m_new);
-      lsum += pw[i];
+  for (int e = 1; e < 8; ++e)
+    mx = fmaxf(mx, sc[e]);
+  mx = max_halves(max_row_pairs(mx));  // over the 4 row groups: all 32 keys
+  const float m_new = fmaxf(m_run, mx);
+  const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;  // nothing visible yet
+  const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+  float ps = 0.f;
+  uint32_t pw[3][4];  // p = hi + mid + lo, each bf16 (the residuals are exact)
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float p0 = __builtin_amdgcn_exp2f(sc[2 * q] - m_use);
+    float p1 = __builtin_amdgcn_exp2f(sc[2 * q + 1] - m_use);
+    ps += p0;
+    ps += p1;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const uint16_t b0 = f2bf(p0), b1 = f2bf(p1);
+      pw[k][q] = uint32_t(b0) | (uint32_t(b1) << 16);
+      p0 -= bf2f(b0);
+      p1 -= bf2f(b1);
     }
-    l_run[h] = l_run[h] * corr + lsum;
+  }
+  l_run = l_run * corr + ps;
+  m_run = m_new;
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o_run[h][e] *= corr;
+  for (int dt = 0; dt < 8; ++dt) {
+    o[dt] *= corr;
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      float vf[8];
-      unpack8(vr[i], vf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        o_run[h][e] = fmaf(pw[i], vf[e], o_run[h][e]);
-    }
-    m_run[h] = m_new;
+    for (int k = 0; k < 3; ++k)
+      o[dt] = mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[dt]);
   }
   if (more)
-    load_v(vc, t0 + kPass, wave, grp, sub, last_cached, vr);
+    load_v(vc, t0 + kPass, wave, lane, last_cached, vr);
 }
 
-// All passes of [s0, s1) for this wave, starting from kr / vr holding the
-// first pass; leaves the wave's (m, l, o) in LDS (w_m, w_l, w_o).
+// All passes of [s0, s1) for this wave (s0 a multiple of 32), starting from
+// kr / vr holding the first pass; leaves the wave's (m, l, o) in LDS (w_m,
+// w_l, w_o). Needs the prologue's q in LDS (after a barrier).
 template <int G>
 __device__ __forceinline__ void split(Lds<G> &sh, const u32x4 *kc, const u32x4 *vc, int s0,
                                       int s1, int pos, int last_cached, int lane, int wave,
-                                      u32x4 (&kr)[kRows], u32x4 (&vr)[kRows]) {
-  const int grp = lane >> 4, sub = lane & 15;
-  float m_run[G], l_run[G], o_run[G][8];
+                                      float qscale, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
+  const int r = lane >> 4, i = lane & 15;
+  u32x4 qb[4];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m_run[h] = -__builtin_inff();
-    l_run[h] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o_run[h][e] = 0.f;
+  for (int s = 0; s < 4; ++s) {
+    const u32x4 v = sh.q[i < G ? i : 0][4 * s + r];
+    qb[s] = i < G ? v : u32x4{0u, 0u, 0u, 0u};
   }
+  float m_run = -__builtin_inff(), l_run = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int t0 = s0;; t0 += kPass) {
     const bool more = t0 + kPass < s1;  // uniform
-    pass<G>(sh, kc, vc, t0, s1, pos, last_cached, more, wave, grp, sub, kr, vr, m_run, l_run,
-            o_run);
+    pass<G>(sh, kc, vc, t0, s1, pos, last_cached, more, wave, lane, qb, qscale, kr, vr, m_run,
+            l_run, o);
     if (!more)
       break;
   }
-  // reduce the four 16-lane groups of the wave
+  const float l = sum_halves(sum_row_pairs(l_run));  // over the 4 row groups
+  if (i < G) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float l = sum_halves(sum_row_pairs(l_run[h]));
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      o_run[h][e] = sum_halves(sum_row_pairs(o_run[h][e]));
-    if (lane < 16) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        sh.w_o[wave][h][sub * 8 + e] = o_run[h][e];
-    }
-    if (lane == 0) {
-      sh.w_m[wave][h] = m_run[h];
-      sh.w_l[wave][h] = l;
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f32x4 *>(&sh.w_o[wave][i][16 * dt + 4 * r]) = o[dt];
+    if (r == 0) {
+      sh.w_m[wave][i] = m_run;
+      sh.w_l[wave][i] = l;
     }
   }
 }

@@ -510,7 +510,6 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
                            uint32_t *part_ml, const int32_t *wait_ctr, int wait_target,
                            int32_t *signal, unsigned long long *tr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int grp = lane >> 4, sub = lane & 15;
   const int Hkv = p.Hkv, S = p.max_splits;
   const int ntasks = B * Hkv * S;
   const float qscale = p.attn_scale * attn::kLog2e;
@@ -523,16 +522,16 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
     const bool valid = pos >= 0 && pos < p.cap;
     const int L = pos + 1;
     const int per = (L + S - 1) / S;
-    const int chunk = (per + 15) & ~15;
+    const int chunk = (per + attn::kBlock - 1) & ~(attn::kBlock - 1);
     const int s0 = s * chunk, s1 = min(L, s0 + chunk);
     const bool active = valid && s0 < s1;
     const size_t head_base = ((size_t(l) * B + b) * Hkv + kvh) * p.cap;
     const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.kc) + head_base * (D / 8);
     const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.vc) + head_base * (D / 8);
     const int last_cached = active && pos > 0 ? pos - 1 : 0;
-    u32x4 kr[attn::kRows], vr[attn::kRows];  // first pass: cached keys only, no dependency
-    attn::load_k(kc, s0, wave, grp, sub, last_cached, kr);
-    attn::load_v(vc, s0, wave, grp, sub, last_cached, vr);
+    u32x4 kr[8], vr[8];  // first pass: cached keys only, no dependency
+    attn::load_k(kc, s0, wave, lane, last_cached, kr);
+    attn::load_v(vc, s0, wave, lane, last_cached, vr);
     if (!waited) {
       wg_wait(wait_ctr, wait_target, cx);
       waited = true;
@@ -553,16 +552,20 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
         }
         attn::prologue_head<G>(sh.at, h, (pr.x & 0xffffu) | (pr.y << 16),
                                (const GLB uint16_t *)(h < G ? Lw.q_norm : Lw.k_norm), p.eps, cs,
-                               sn, qscale, lane);
+                               sn, lane);
       }
       __syncthreads();
-      if (pos >= s0 && pos < s1 && threadIdx.x < 2 * (D / 8)) {  // append (ar.cpp:119-123)
-        const int which = threadIdx.x / (D / 8), c = threadIdx.x % (D / 8);
-        u32x4 *dst = reinterpret_cast<u32x4 *>(which ? p.vc : p.kc) +
-                     (head_base + pos) * (D / 8) + c;
-        *dst = sh.at.kv_new[which][c];
+      if (pos >= s0 && pos < s1 && threadIdx.x < D / 8 + D) {  // append (ar.cpp:119-123)
+        if (threadIdx.x < D / 8) {
+          reinterpret_cast<u32x4 *>(p.kc)[(head_base + pos) * (D / 8) + threadIdx.x] =
+              sh.at.kv_new[0][threadIdx.x];
+        } else {
+          const int d = threadIdx.x - D / 8;
+          p.vc[head_base * D + attn::v_index(pos, d)] =
+              reinterpret_cast<const uint16_t *>(&sh.at.kv_new[1][0])[d];
+        }
       }
-      attn::split<G>(sh.at, kc, vc, s0, s1, pos, last_cached, lane, wave, kr, vr);
+      attn::split<G>(sh.at, kc, vc, s0, s1, pos, last_cached, lane, wave, qscale, kr, vr);
       __syncthreads();
       const size_t part = (size_t(b) * Hkv + kvh) * S + s;
       for (int e = threadIdx.x; e < G * D; e += 256) {
@@ -616,7 +619,7 @@ __device__ void merge_phase(SH &sh, const DecodeParams &p, const Ctx &cx,
     const bool valid = pos >= 0 && pos < p.cap;
     const int L = pos + 1;
     const int per = (L + S - 1) / S;
-    const int chunk = (per + 15) & ~15;
+    const int chunk = (per + attn::kBlock - 1) & ~(attn::kBlock - 1);
     const int n_active = valid ? min(max((L + chunk - 1) / chunk, 1), S) : 1;
     const size_t part0 = (size_t(b) * Hkv + kvh) * S;
     if (!waited) {

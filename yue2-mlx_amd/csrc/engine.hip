@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "../../include/yuear.h"
+#include "attn_core.h"
 #include "common.h"
 #include "decode.h"
 #include "kernels.h"
@@ -304,10 +305,13 @@ struct yuear_engine {
 struct yuear_session {
   yuear_engine *e = nullptr;
   int B = 1, cap = 0, max_splits = 1;
+  int kv_stride = 0;  // slots per (layer, branch, kv head): cap rounded up to a V block
   PhaseInfo phase{};
   hipStream_t stream = nullptr;
   // device state
-  uint16_t *kc = nullptr, *vc = nullptr;  // [layers][B][Hkv][cap][D]
+  // [layers][B][Hkv] x kv_stride slots; K row-major, V in 32-slot dim-major
+  // blocks (attn::v_index)
+  uint16_t *kc = nullptr, *vc = nullptr;
   int32_t *pos = nullptr, *tok = nullptr;
   uint16_t *x = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
   float *part_o = nullptr, *part_ml = nullptr;
@@ -363,7 +367,7 @@ struct yuear_session {
   }
   size_t layer_kv_offset(int layer, int branch) const {
     const Config &c = e->cfg;
-    return (size_t(layer) * B + branch) * c.Hkv * size_t(cap) * c.D;
+    return (size_t(layer) * B + branch) * c.Hkv * size_t(kv_stride) * c.D;
   }
 };
 
@@ -514,10 +518,11 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.e = E;
   S.B = branches;
   S.cap = capacity;
+  S.kv_stride = (capacity + attn::kBlock - 1) / attn::kBlock * attn::kBlock;
   S.phase = phase_info(phase, c.V);
   HIPC(hipSetDevice(E->device));
   HIPC(hipStreamCreateWithFlags(&S.stream, hipStreamNonBlocking));
-  const size_t kv = size_t(c.layers) * branches * c.Hkv * size_t(capacity) * c.D;
+  const size_t kv = size_t(c.layers) * branches * c.Hkv * size_t(S.kv_stride) * c.D;
   S.kc = S.alloc<uint16_t>(kv);
   S.vc = S.alloc<uint16_t>(kv);
   // zero-filled like mx::zeros (ar.cpp:113-118); done once at allocation
@@ -532,13 +537,14 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.attn = S.alloc<uint16_t>(size_t(branches) * c.Hq * c.D);
   S.act = S.alloc<uint16_t>(size_t(branches) * c.F);
   S.logits = S.alloc<uint16_t>(size_t(branches) * S.phase.stride());
-  // split-K: up to 64 splits of >= 128 keys (256 workgroups at KV 4096,
-  // batch 1, 8 kv heads); YUEAR_ATTN_KEYS_PER_SPLIT overrides the target
+  // split-K: about 192 workgroups over all branches and kv heads (24 splits
+  // at batch 1 with 8 kv heads, 3 at batch 8), never more splits than 32-key
+  // blocks; measured best on MI355X at KV 1k-8k. YUEAR_ATTN_SPLITS overrides.
   {
-    int keys = 128;
-    if (const char *env = std::getenv("YUEAR_ATTN_KEYS_PER_SPLIT"))
-      keys = std::max(16, std::atoi(env));
-    S.max_splits = std::max(1, std::min(64, (capacity + keys - 1) / keys));
+    int splits = (192 + branches * c.Hkv - 1) / (branches * c.Hkv);
+    if (const char *env = std::getenv("YUEAR_ATTN_SPLITS"))
+      splits = std::atoi(env);
+    S.max_splits = std::max(1, std::min({64, splits, S.kv_stride / attn::kBlock}));
   }
   const int G = c.Hq / c.Hkv;
   S.part_o = S.alloc<float>(size_t(branches) * c.Hkv * S.max_splits * G * c.D);
@@ -663,7 +669,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   a.heads = c.Hq;
   a.kv_heads = c.Hkv;
   a.head_dim = c.D;
-  a.capacity = S.cap;
+  a.capacity = S.kv_stride;
   a.batch = S.B;
   a.max_splits = S.max_splits;
   a.part_o = S.part_o;
@@ -766,7 +772,7 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
     a.q_norm = c.qk_norm ? L.q_norm : nullptr; a.k_norm = c.qk_norm ? L.k_norm : nullptr;
     a.eps = c.eps; a.rope_cos = E.rope_cos; a.rope_sin = E.rope_sin;
     a.k_cache = S.kc + S.layer_kv_offset(l, 0); a.v_cache = S.vc + S.layer_kv_offset(l, 0);
-    a.pos = S.pos; a.heads = c.Hq; a.kv_heads = c.Hkv; a.head_dim = c.D; a.capacity = S.cap;
+    a.pos = S.pos; a.heads = c.Hq; a.kv_heads = c.Hkv; a.head_dim = c.D; a.capacity = S.kv_stride;
     a.batch = S.B; a.max_splits = S.max_splits; a.part_o = S.part_o; a.part_ml = S.part_ml;
     a.counters = S.counters; a.out = S.attn; a.out_stride = c.Hq * c.D;
     HIPC(launch_attn_decode(a, S.stream));
@@ -788,7 +794,7 @@ DecodeParams decode_params(yuear_session &S) {
   p.embed = E.embed; p.lm_head = E.lm_head; p.final_norm = E.final_norm;
   p.rope_cos = E.rope_cos; p.rope_sin = E.rope_sin;
   p.layers = S.dlayers;
-  p.kc = S.kc; p.vc = S.vc; p.cap = S.cap;
+  p.kc = S.kc; p.vc = S.vc; p.cap = S.kv_stride;
   p.pos = S.pos; p.tok = S.tok;
   p.xs = S.dxs; p.qkv = S.dqkv; p.qkv_stride = c.qkv(); p.attn = S.dattn; p.act = S.dact;
   p.part_o = S.dpart_o; p.part_ml = S.dpart_ml; p.max_splits = S.max_splits;
@@ -904,7 +910,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       qp.heads = c.Hq;
       qp.kv_heads = c.Hkv;
       qp.head_dim = c.D;
-      qp.capacity = S.cap;
+      qp.capacity = S.kv_stride;
       qp.q_out = S.pq;
       qp.k_cache = S.kc + S.layer_kv_offset(l, b);
       qp.v_cache = S.vc + S.layer_kv_offset(l, b);
@@ -918,7 +924,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       ap.heads = c.Hq;
       ap.kv_heads = c.Hkv;
       ap.head_dim = c.D;
-      ap.capacity = S.cap;
+      ap.capacity = S.kv_stride;
       ap.out = S.pattn;
       HIPC(launch_attn_prefill(ap, st));
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
@@ -1155,12 +1161,20 @@ yuear_status yuear_session_write_kv(yuear_session *S, int32_t layer, int32_t bra
     const Config &c = S->e->cfg;
     if (layer < 0 || layer >= c.layers || branch < 0 || branch >= S->B || n < 0 || n > S->cap)
       invalid("layer/branch/length out of range");
+    // V goes into the cache's block layout: whole blocks covering [0, n),
+    // slots past n zero (invisible: the position becomes n)
+    const int nb = (n + attn::kBlock - 1) / attn::kBlock * attn::kBlock;
+    std::vector<uint16_t> vb(size_t(nb) * c.D);
+    HIPC(hipStreamSynchronize(S->stream));
     for (int h = 0; h < c.Hkv; ++h) {
-      const size_t off = S->layer_kv_offset(layer, branch) + size_t(h) * S->cap * c.D;
+      const size_t off = S->layer_kv_offset(layer, branch) + size_t(h) * S->kv_stride * c.D;
       HIPC(hipMemcpy(S->kc + off, k + size_t(h) * n * c.D, size_t(n) * c.D * 2,
                      hipMemcpyHostToDevice));
-      HIPC(hipMemcpy(S->vc + off, v + size_t(h) * n * c.D, size_t(n) * c.D * 2,
-                     hipMemcpyHostToDevice));
+      std::fill(vb.begin(), vb.end(), uint16_t(0));
+      for (int t = 0; t < n; ++t)
+        for (int d = 0; d < c.D; ++d)
+          vb[attn::v_index(t, d)] = v[(size_t(h) * n + t) * c.D + d];
+      HIPC(hipMemcpy(S->vc + off, vb.data(), vb.size() * 2, hipMemcpyHostToDevice));
     }
     S->host_pos[branch] = n;
     set_device_pos(*S);
@@ -1176,12 +1190,16 @@ yuear_status yuear_session_read_kv(yuear_session *S, int32_t layer, int32_t bran
     if (layer < 0 || layer >= c.layers || branch < 0 || branch >= S->B || n < 0 || n > S->cap)
       invalid("layer/branch/length out of range");
     HIPC(hipStreamSynchronize(S->stream));
+    const int nb = (n + attn::kBlock - 1) / attn::kBlock * attn::kBlock;
+    std::vector<uint16_t> vb(size_t(nb) * c.D);
     for (int h = 0; h < c.Hkv; ++h) {
-      const size_t off = S->layer_kv_offset(layer, branch) + size_t(h) * S->cap * c.D;
+      const size_t off = S->layer_kv_offset(layer, branch) + size_t(h) * S->kv_stride * c.D;
       HIPC(hipMemcpy(k + size_t(h) * n * c.D, S->kc + off, size_t(n) * c.D * 2,
                      hipMemcpyDeviceToHost));
-      HIPC(hipMemcpy(v + size_t(h) * n * c.D, S->vc + off, size_t(n) * c.D * 2,
-                     hipMemcpyDeviceToHost));
+      HIPC(hipMemcpy(vb.data(), S->vc + off, vb.size() * 2, hipMemcpyDeviceToHost));
+      for (int t = 0; t < n; ++t)
+        for (int d = 0; d < c.D; ++d)
+          v[(size_t(h) * n + t) * c.D + d] = vb[attn::v_index(t, d)];
     }
   });
 }

@@ -38,6 +38,10 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
 bool gemv_mfma_supported(const GemvParams &p);
 hipError_t launch_gemv_mfma(const GemvParams &p, hipStream_t s);
 
+// KV cache layout of one (branch, kv head), `capacity` slots (a multiple of
+// 32): K row-major [capacity][128]; V in 32-slot blocks stored dim-major,
+// element (t, d) at attn::v_index(t, d) = (t / 32) * 4096 + d * 32 + t % 32.
+
 // Split-K flash-decode attention for one layer, all branches, with the
 // q/k RMSNorm + RoPE prologue, the KV append of the current token and the
 // last-block merge of the split partials fused in.
@@ -47,7 +51,7 @@ struct AttnDecodeParams {
   const uint16_t *q_norm = nullptr, *k_norm = nullptr;  // [D] or null
   float eps = 1e-6f;
   const uint16_t *rope_cos = nullptr, *rope_sin = nullptr;  // [positions][D/2]
-  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [batch][Hkv][cap][D]
+  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [batch][Hkv] x (capacity slots)
   const int32_t *pos = nullptr;  // [batch] slot of the current token
   int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0, batch = 1;
   int max_splits = 1;
@@ -124,7 +128,7 @@ struct QkPrepParams {
   int pos0 = 0;
   int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0;
   uint16_t *q_out = nullptr;  // [T][Hq][D]
-  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // this branch [Hkv][cap][D]
+  uint16_t *k_cache = nullptr, *v_cache = nullptr;  // this branch, [Hkv] x (capacity slots)
 };
 hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s);
 
@@ -132,7 +136,7 @@ hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s);
 // with fp32 opmath (ar.cpp:284-291). out [T][Hq*D].
 struct AttnPrefillParams {
   const uint16_t *q = nullptr;  // [T][Hq][D]
-  const uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [Hkv][cap][D]
+  const uint16_t *k_cache = nullptr, *v_cache = nullptr;  // [Hkv] x (capacity slots)
   int tokens = 0, pos0 = 0;
   int heads = 0, kv_heads = 0, head_dim = 128, capacity = 0;
   uint16_t *out = nullptr;

@@ -8,6 +8,7 @@
 // scores, softmax and P.V in fp32 and rounds only the output to bf16.
 #include <cmath>
 
+#include "attn_core.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -203,9 +204,12 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
       const int kvh = h - p.heads;
       norm_rope_head(y0, y1, p.k_norm, p.eps, cs, sn, lane, y0, y1);
       dst = reinterpret_cast<uint32_t *>(p.k_cache + (size_t(kvh) * p.capacity + pos) * 128);
-    } else {
+    } else {  // V: dims 2 lane, 2 lane + 1 into the slot's 32-key block column
       const int kvh = h - p.heads - p.kv_heads;
-      dst = reinterpret_cast<uint32_t *>(p.v_cache + (size_t(kvh) * p.capacity + pos) * 128);
+      uint16_t *vh = p.v_cache + size_t(kvh) * p.capacity * 128;
+      vh[attn::v_index(pos, 2 * lane)] = f2bf(y0);
+      vh[attn::v_index(pos, 2 * lane + 1)] = f2bf(y1);
+      continue;
     }
     dst[lane] = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
   }
@@ -254,7 +258,19 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p, 
       const int idx = tid + 256 * c, r = idx >> 4, col = idx & 15;
       const int key = min(kt + r, kend - 1);
       ks[r][col] = kc[size_t(key) * 16 + col];
-      vs[r][col] = vc[size_t(key) * 16 + col];
+      // V: 16 bytes = 8 keys of one dim of a 32-key block, transposed into
+      // vs[key][dim]; a block past the last visible key's block is clamped
+      // (all its keys are masked)
+      const int half = idx >> 9, d = (idx >> 2) & 127, q = idx & 3;
+      const int blk = min((kt >> 5) + half, (kend - 1) >> 5);
+      const u32x4 v = vc[size_t(blk) * 512 + d * 4 + q];
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+      uint16_t *vs16 = reinterpret_cast<uint16_t *>(&vs[0][0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vs16[(32 * half + 8 * q + 2 * e) * 128 + d] = uint16_t(vw[e]);
+        vs16[(32 * half + 8 * q + 2 * e + 1) * 128 + d] = uint16_t(vw[e] >> 16);
+      }
     }
     __syncthreads();
     float s[64];
@@ -344,7 +360,8 @@ hipError_t launch_swiglu_rows(const uint16_t *gu, int rows, int f, uint16_t *out
 }
 
 hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
-  if (p.head_dim != 128 || p.tokens < 1 || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity)
+  if (p.head_dim != 128 || p.tokens < 1 || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity ||
+      p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const int nh = p.heads + 2 * p.kv_heads;
   const int gy = (nh + 3) / 4;
@@ -354,7 +371,7 @@ hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
 
 hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s) {
   if (p.head_dim != 128 || p.tokens < 1 || p.kv_heads < 1 || p.heads % p.kv_heads ||
-      p.pos0 + p.tokens > p.capacity)
+      p.pos0 + p.tokens > p.capacity || p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const float qscale = float(std::pow(128.0, -0.5)) * 1.4426950408889634f;
   hipLaunchKernelGGL(attn_prefill_kernel, dim3((p.tokens + 63) / 64, p.heads), dim3(256), 0, s, p,

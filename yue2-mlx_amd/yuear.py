@@ -196,6 +196,34 @@ def random_weights(config, seed, std=0.02, norm_std=0.0):
             for name, shape in tensor_shapes(config).items()}
 
 
+V_BLOCK = 32  # slots per block of the V cache layout
+
+
+def kv_slots(capacity):
+    """Slots per kv head of a cache of `capacity` positions (whole V blocks)."""
+    return (capacity + V_BLOCK - 1) // V_BLOCK * V_BLOCK
+
+
+def v_blocked(v):
+    """[..., slots, 128] values (slots a multiple of 32) -> the V cache layout
+    of the op-level attention entry points: 32-slot blocks stored dim-major,
+    element (t, d) at (t // 32) * 4096 + d * 32 + t % 32 (same shape)."""
+    v = np.asarray(v)
+    *lead, n, d = v.shape
+    if n % V_BLOCK:
+        raise ValueError("slots must be a multiple of 32")
+    return np.ascontiguousarray(
+        v.reshape(*lead, n // V_BLOCK, V_BLOCK, d).swapaxes(-1, -2)).reshape(*lead, n, d)
+
+
+def v_unblocked(vb):
+    """Inverse of v_blocked."""
+    vb = np.asarray(vb)
+    *lead, n, d = vb.shape
+    return np.ascontiguousarray(
+        vb.reshape(*lead, n // V_BLOCK, d, V_BLOCK).swapaxes(-1, -2)).reshape(*lead, n, d)
+
+
 def rope_table(positions, head_dim, theta):
     c = np.empty((positions, head_dim // 2), dtype=np.uint16)
     s = np.empty_like(c)
