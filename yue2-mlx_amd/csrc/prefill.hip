@@ -1,11 +1,12 @@
 // Prompt prefill kernels on gfx950: MFMA bf16 GEMM for the projections,
 // row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV append, and
-// a causal attention with fp32 opmath.
+// an MFMA causal attention with fp32 opmath.
 //
 // Reference: native/src/ar.cpp:246-301 (hidden() over T > 1 tokens) and
 // native/src/sampling.cpp:152-183 (prefill). The reference upcasts Q/K/V to
-// fp32 for the causal SDPA (ar.cpp:284-291); the attention kernel here keeps
-// scores, softmax and P.V in fp32 and rounds only the output to bf16.
+// fp32 for the causal SDPA (ar.cpp:284-291); the attention kernel here forms
+// exact products on MFMA, keeps scores, softmax and all sums in fp32 and
+// rounds only the output to bf16.
 #include <cmath>
 
 #include "attn_core.h"
@@ -216,113 +217,141 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention, fp32 opmath. Block (64 queries, one q head), 4 threads per
-// query each owning 32 of the 128 dims; 64-key tiles staged in LDS; the
-// current tile's 64 scores are kept in registers for an exact per-tile
-// online softmax (exp2 with log2(e) folded into q).
+// Causal attention on MFMA (ar.cpp:284-291: fp32 scores, softmax and P.V,
+// bf16 output). Workgroup = 4 independent waves on one q head; wave w owns
+// queries q0 = 128 blockIdx.y' + 32 w + [0, 32) as two 16-query MFMA column
+// tiles and walks the 32-key V blocks of its causal range [0, pos0 + last
+// query], one block per step with the next block's K/V loads in flight:
+//
+//   S^T[key][query] = K[key][:] . q[query][:]     (attn_core.h row order)
+//   O^T[dim][query] += V^T[dim][key] . P^T[key][query]   P as hi + mid + lo
+//
+// the decode core's arithmetic with the queries as MFMA columns. Products
+// are exact and all sums fp32; the output is bf16(o / l) as in the
+// reference. Query tiles are dispatched longest first (the causal tail), and
+// all heads of a tile run together so K/V blocks are shared in L2.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
-  __shared__ u32x4 ks[64][16];
-  __shared__ u32x4 vs[64][16];
-  const int tid = threadIdx.x, qi = tid >> 2, part = tid & 3;
-  const int h = blockIdx.y, kvh = h / (p.heads / p.kv_heads);
-  const int q_idx = blockIdx.x * 64 + qi;
-  const bool valid = q_idx < p.tokens;
-  const int qpos = p.pos0 + (valid ? q_idx : p.tokens - 1);
-  const int kend = p.pos0 + min(p.tokens, blockIdx.x * 64 + 64);  // keys [0, kend)
-  float q[32];
-  {
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(
-        p.q + (size_t(valid ? q_idx : 0) * p.heads + h) * 128 + part * 32);
+  using attn::D;
+  using attn::f32x4;
+  using attn::kBlock;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane >> 4, i = lane & 15;
+  const int h = blockIdx.x;
+  const int tile = gridDim.y - 1 - blockIdx.y;  // longest causal range first
+  const int qbase = tile * 128 + wave * 32;
+  if (qbase >= p.tokens)
+    return;  // whole wave idle (no barriers in this kernel)
+  const int kvh = h / (p.heads / p.kv_heads);
+  const int kend = p.pos0 + min(qbase + 32, p.tokens);  // keys [0, kend)
+  const int last = kend - 1;
+  const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.k_cache) + size_t(kvh) * p.capacity * (D / 8);
+  const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.v_cache) + size_t(kvh) * p.capacity * (D / 8);
+
+  // Q^T operands: column tile c, query qbase + 16 c + i (clamped), dims 32 s + 8 r
+  u32x4 qb[2][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 v = src[c];
-      const uint32_t vi[4] = {v.x, v.y, v.z, v.w};
+  for (int c = 0; c < 2; ++c) {
+    const int qi = min(qbase + 16 * c + i, p.tokens - 1);
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(p.q + (size_t(qi) * p.heads + h) * D);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        q[c * 8 + 2 * e] = bflo(vi[e]) * qscale;
-        q[c * 8 + 2 * e + 1] = bfhi(vi[e]) * qscale;
+    for (int s = 0; s < 4; ++s)
+      qb[c][s] = src[4 * s + r];
+  }
+  u32x4 kr[8], vr[8];
+  attn::load_k(kc, 0, 0, lane, last, kr);
+  attn::load_v(vc, 0, 0, lane, last, vr);
+
+  float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
+  f32x4 o[2][8];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      o[c][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < kend; kb += kBlock) {
+    const bool more = kb + kBlock < kend;  // uniform
+    u32x4 kn[8], vn[8];
+    if (more) {
+      attn::load_k(kc, kb + kBlock, 0, lane, last, kn);
+      attn::load_v(vc, kb + kBlock, 0, lane, last, vn);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      f32x4 st[2];
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        st[T] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          st[T] = attn::mfma(kr[4 * T + s], qb[c][s], st[T]);
+      }
+      // lane (query qbase + 16 c + i, r): keys kb + 8 r + 4 T + t, visible up
+      // to the query's own position pos0 + q
+      const int qpos = p.pos0 + qbase + 16 * c + i;
+      float sc[8];
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          sc[4 * T + t] = kb + 8 * r + 4 * T + t <= qpos ? st[T][t] * qscale : -__builtin_inff();
+      float mx = sc[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e)
+        mx = fmaxf(mx, sc[e]);
+      mx = max_halves(max_row_pairs(mx));
+      const float m_new = fmaxf(m_run[c], mx);
+      const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+      const float corr = __builtin_amdgcn_exp2f(m_run[c] - m_use);
+      float ps = 0.f;
+      uint32_t pw[3][4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float p0 = __builtin_amdgcn_exp2f(sc[2 * q] - m_use);
+        float p1 = __builtin_amdgcn_exp2f(sc[2 * q + 1] - m_use);
+        ps += p0;
+        ps += p1;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const uint16_t b0 = f2bf(p0), b1 = f2bf(p1);
+          pw[k][q] = uint32_t(b0) | (uint32_t(b1) << 16);
+          p0 -= bf2f(b0);
+          p1 -= bf2f(b1);
+        }
+      }
+      l_run[c] = l_run[c] * corr + ps;
+      m_run[c] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        o[c][dt] *= corr;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          o[c][dt] = attn::mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[c][dt]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kr[j] = kn[j];
+        vr[j] = vn[j];
       }
     }
   }
-  const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.k_cache) + size_t(kvh) * p.capacity * 16;
-  const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.v_cache) + size_t(kvh) * p.capacity * 16;
-  float m = -__builtin_inff(), l = 0.f, o[32];
+  // lane (query, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
 #pragma unroll
-  for (int d = 0; d < 32; ++d)
-    o[d] = 0.f;
-  for (int kt = 0; kt < kend; kt += 64) {
-    __syncthreads();
+  for (int c = 0; c < 2; ++c) {
+    const float l = sum_halves(sum_row_pairs(l_run[c]));
+    const int qi = qbase + 16 * c + i;
+    if (qi < p.tokens) {
+      uint16_t *dst = p.out + size_t(qi) * p.heads * D + size_t(h) * D;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 256 * c, r = idx >> 4, col = idx & 15;
-      const int key = min(kt + r, kend - 1);
-      ks[r][col] = kc[size_t(key) * 16 + col];
-      // V: 16 bytes = 8 keys of one dim of a 32-key block, transposed into
-      // vs[key][dim]; a block past the last visible key's block is clamped
-      // (all its keys are masked)
-      const int half = idx >> 9, d = (idx >> 2) & 127, q = idx & 3;
-      const int blk = min((kt >> 5) + half, (kend - 1) >> 5);
-      const u32x4 v = vc[size_t(blk) * 512 + d * 4 + q];
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-      uint16_t *vs16 = reinterpret_cast<uint16_t *>(&vs[0][0]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vs16[(32 * half + 8 * q + 2 * e) * 128 + d] = uint16_t(vw[e]);
-        vs16[(32 * half + 8 * q + 2 * e + 1) * 128 + d] = uint16_t(vw[e] >> 16);
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint32_t lo = uint32_t(f2bf(o[c][dt][0] / l)) | (uint32_t(f2bf(o[c][dt][1] / l)) << 16);
+        const uint32_t hi = uint32_t(f2bf(o[c][dt][2] / l)) | (uint32_t(f2bf(o[c][dt][3] / l)) << 16);
+        *reinterpret_cast<uint2 *>(dst + 16 * dt + 4 * r) = uint2{lo, hi};
       }
     }
-    __syncthreads();
-    float s[64];
-    float mt = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      float a = 0.f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 v = ks[j][part * 4 + c];
-        const uint32_t vi[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a = fmaf(q[c * 8 + 2 * e], bflo(vi[e]), a);
-          a = fmaf(q[c * 8 + 2 * e + 1], bfhi(vi[e]), a);
-        }
-      }
-      a += __shfl_xor(a, 1, 64);
-      a += __shfl_xor(a, 2, 64);
-      s[j] = kt + j <= qpos ? a : -__builtin_inff();
-      mt = fmaxf(mt, s[j]);
-    }
-    const float m_new = fmaxf(m, mt);
-    const float corr = __builtin_amdgcn_exp2f(m - m_new);
-    l *= corr;
-#pragma unroll
-    for (int d = 0; d < 32; ++d)
-      o[d] *= corr;
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      const float pj = __builtin_amdgcn_exp2f(s[j] - m_new);
-      l += pj;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 v = vs[j][part * 4 + c];
-        const uint32_t vi[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[c * 8 + 2 * e] = fmaf(pj, bflo(vi[e]), o[c * 8 + 2 * e]);
-          o[c * 8 + 2 * e + 1] = fmaf(pj, bfhi(vi[e]), o[c * 8 + 2 * e + 1]);
-        }
-      }
-    }
-    m = m_new;
-  }
-  if (valid) {
-    uint32_t *dst = reinterpret_cast<uint32_t *>(p.out + size_t(q_idx) * p.heads * 128 + h * 128 +
-                                                 part * 32);
-    const float inv = 1.0f / l;
-#pragma unroll
-    for (int d = 0; d < 16; ++d)
-      dst[d] = uint32_t(f2bf(o[2 * d] * inv)) | (uint32_t(f2bf(o[2 * d + 1] * inv)) << 16);
   }
 }
 
@@ -374,8 +403,8 @@ hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s) {
       p.pos0 + p.tokens > p.capacity || p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const float qscale = float(std::pow(128.0, -0.5)) * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3((p.tokens + 63) / 64, p.heads), dim3(256), 0, s, p,
-                     qscale);
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(p.heads, (p.tokens + 127) / 128), dim3(256), 0, s,
+                     p, qscale);
   return hipGetLastError();
 }
 
