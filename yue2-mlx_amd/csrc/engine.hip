@@ -314,6 +314,7 @@ struct yuear_session {
   uint16_t *kc = nullptr, *vc = nullptr;
   int32_t *pos = nullptr, *tok = nullptr;
   uint16_t *x = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+  uint16_t *stage = nullptr;  // [B][H] prepared (gathered / normalised) rows, batched GEMVs
   float *part_o = nullptr, *part_ml = nullptr;
   int32_t *counters = nullptr;
   float *scratch = nullptr, *alphas = nullptr;
@@ -533,6 +534,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   HIPC(hipMemsetAsync(S.pos, 0, branches * 4, S.stream));
   HIPC(hipMemsetAsync(S.tok, 0, branches * 4, S.stream));
   S.x = S.alloc<uint16_t>(size_t(branches) * c.H);
+  S.stage = S.alloc<uint16_t>(size_t(branches) * c.H);
   S.qkv = S.alloc<uint16_t>(size_t(branches) * c.qkv());
   S.attn = S.alloc<uint16_t>(size_t(branches) * c.Hq * c.D);
   S.act = S.alloc<uint16_t>(size_t(branches) * c.F);
@@ -651,6 +653,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   }
   q.norm_w = L.input_ln;
   q.eps = c.eps;
+  q.stage = S.stage;
   q.y = S.qkv;
   q.y_stride = c.qkv();
   HIPC(launch_gemv(q, st));
@@ -700,6 +703,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   g.x_stride = c.H;
   g.norm_w = L.post_ln;
   g.eps = c.eps;
+  g.stage = S.stage;
   g.y = S.act;
   g.y_stride = c.F;
   g.epilogue = kEpiSwiGLU;
@@ -733,6 +737,7 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   h.x_stride = x_stride;
   h.norm_w = E.final_norm;
   h.eps = c.eps;
+  h.stage = batch <= S.B ? S.stage : nullptr;
   h.y = out;
   h.y_stride = S.phase.stride();
   h.seg0_start = S.phase.seg0_start;
@@ -753,13 +758,14 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
   g.eps = c.eps;
   if (which == "qkv") {
     g.w = L.qkv; g.n = c.qkv(); g.k = c.H; g.x = S.x; g.x_stride = c.H;
-    g.norm_w = L.input_ln; g.y = S.qkv; g.y_stride = c.qkv();
+    g.norm_w = L.input_ln; g.y = S.qkv; g.y_stride = c.qkv(); g.stage = S.stage;
   } else if (which == "o_proj") {
     g.w = L.o; g.n = c.H; g.k = c.Hq * c.D; g.x = S.attn; g.x_stride = c.Hq * c.D;
     g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual;
   } else if (which == "gate_up") {
     g.w = L.gu; g.n = 2 * c.F; g.k = c.H; g.x = S.x; g.x_stride = c.H;
     g.norm_w = L.post_ln; g.y = S.act; g.y_stride = c.F; g.epilogue = kEpiSwiGLU;
+    g.stage = S.stage;
   } else if (which == "down") {
     g.w = L.down; g.n = c.H; g.k = c.F; g.x = S.act; g.x_stride = c.F;
     g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual;
@@ -1615,6 +1621,24 @@ int32_t yuear_op_gemv(const uint16_t *w, int32_t n, int32_t k, int32_t batch, co
   p.y = y;
   p.y_stride = y_stride;
   p.epilogue = epilogue;
+  if (batch >= 3 && norm_w && k > 0) {
+    // the batched form normalises the rows once into a scratch buffer,
+    // owned by a small per-process pool like the attention partials
+    static std::mutex mu;
+    static uint16_t *stage = nullptr;
+    static size_t stage_elems = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    const size_t need = size_t(batch) * k;
+    if (need > stage_elems) {
+      if (stage) (void)hipFree(stage);
+      stage = nullptr;
+      stage_elems = 0;
+      if (hipMalloc(&stage, need * 2) != hipSuccess) return int32_t(hipErrorOutOfMemory);
+      stage_elems = need;
+    }
+    p.stage = stage;
+    return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
+  }
   return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
 }
 

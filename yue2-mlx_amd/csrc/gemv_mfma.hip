@@ -14,14 +14,16 @@
 // from the staged activations; D = 16 rows x 16 columns, lane l holding
 // column l % 16, rows 4 (l / 16) + [0, 4).
 //
-// Order: the activation loads are issued first, then all KSTEPS weight loads
-// of the wave (non-temporal), so the activation staging waits only for the
-// former (the vector-memory counter drains in issue order). Activations are
-// staged in LDS with rows padded by 16 bytes (conflict-free 16-byte reads
-// across the 16 batch columns), gathered from the embedding for layer 0 and
-// RMS-normalised in place when a gain is given (ar.cpp:30-35 rounding
-// points). The waves' D tiles are summed through LDS in wave order, then the
-// epilogue (store / residual / SwiGLU) runs one thread per (row, column).
+// Rows that need a gather (layer 0's embedding) or an RMSNorm prologue
+// (ar.cpp:30-35) are prepared once by a small row kernel into p.stage;
+// re-normalising all rows in every workgroup costs more than the weight
+// stream it hides behind. In the main kernel each thread first loads one
+// 16-byte activation column of all rows, then all KSTEPS weight loads of its
+// wave (non-temporal), so the staging waits only for the former (the
+// vector-memory counter drains in issue order). Rows are staged in LDS
+// padded by 16 bytes (conflict-free 16-byte reads across the 16 batch
+// columns). The waves' D tiles are summed through LDS in wave order, then
+// the epilogue (store / residual / SwiGLU) runs one thread per (row, column).
 #include "common.h"
 #include "kernels.h"
 
@@ -34,6 +36,62 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// Row preparation for the batched form (grid = batch rows, 256 threads):
+// gather from the embedding (copy-out to x_out) and/or RMSNorm with the
+// rounding points of ar.cpp:30-35, written to p.stage.
+__global__ __launch_bounds__(256) void stage_rows_kernel(GemvParams p) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = p.k >> 3;
+  const uint16_t *src;
+  if (p.embed) {
+    const int t = min(max(p.tokens[b], 0), p.embed_rows - 1);
+    src = p.embed + size_t(t) * p.k;
+  } else {
+    src = p.x + size_t(b) * p.x_stride;
+  }
+  const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
+  u32x4 *dst = reinterpret_cast<u32x4 *>(p.stage + size_t(b) * p.k);
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < nch; c += 256) {
+    const u32x4 v = s4[c];
+    if (p.x_out)
+      reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v;
+    if (!p.norm_w) {
+      dst[c] = v;
+      continue;
+    }
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = bflo(w4[q]), hi = bfhi(w4[q]);
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+  }
+  if (!p.norm_w)
+    return;
+  ss = wave_sum(ss);
+  if (lane == 0)
+    red[wave] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float scale = rbf(1.0f / __builtin_sqrtf(total / float(p.k) + p.eps));
+  const u32x4 *g4 = reinterpret_cast<const u32x4 *>(p.norm_w);
+  for (int c = threadIdx.x; c < nch; c += 256) {
+    const u32x4 v = s4[c], g = g4[c];
+    const uint32_t vi[4] = {v.x, v.y, v.z, v.w}, gi[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = f2bf(rbf(bflo(vi[q]) * scale) * bflo(gi[q]));
+      const uint32_t hi = f2bf(rbf(bfhi(vi[q]) * scale) * bfhi(gi[q]));
+      o[q] = lo | (hi << 16);
+    }
+    dst[c] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 template <int WAVES, int KSTEPS, int EPI>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvParams p) {
   extern __shared__ u32x4 lds[];
@@ -41,30 +99,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvParams p) {
   constexpr int K = WAVES * KSTEPS * 32;
   constexpr int NCH = K / 8;           // 16-byte chunks per activation row
   constexpr int ROWC = NCH + 1;        // staged row stride (chunks): +16 bytes of padding
-  constexpr int XPT = (8 * NCH + NT - 1) / NT;
-  __shared__ float red_ss[8][WAVES];
-  __shared__ float scale_b[8];
+  static_assert(NCH <= NT, "one activation column per thread");
   float *red = reinterpret_cast<float *>(lds + 8 * ROWC);  // [WAVES][16][16]
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int B = p.batch;
   const int n0 = blockIdx.x * 16;
+  const int c = min(int(threadIdx.x), NCH - 1);  // this thread's activation column
 
-  // 1. activation loads (branch-free: clamped, masked later)
-  u32x4 xr[XPT];
+  // 1. activation column c of every row first (rows past the batch clamped)
+  u32x4 xr[8];
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int idx = min(int(threadIdx.x) + NT * i, B * NCH - 1);
-    const int b = idx / NCH, c = idx - b * NCH;
-    const uint16_t *src;
-    if (p.embed) {
-      const int t = min(max(p.tokens[b], 0), p.embed_rows - 1);
-      src = p.embed + size_t(t) * K;
-    } else {
-      src = p.x + size_t(b) * p.x_stride;
-    }
-    xr[i] = reinterpret_cast<const u32x4 *>(src)[c];
-  }
+  for (int b = 0; b < 8; ++b)
+    xr[b] = reinterpret_cast<const u32x4 *>(p.x + size_t(min(b, B - 1)) * p.x_stride)[c];
+  // keep these loads ahead of the weight stream (the scheduler may otherwise
+  // sink some below it, and the staging would then wait for every weight)
+  __builtin_amdgcn_sched_barrier(0);
 
   // 2. this wave's weight stream: row n0 + l % 16 (clamped; mapped for the
   // lm_head phases), k = wave * KW + 32 s + 8 (l / 16)
@@ -79,69 +129,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvParams p) {
       a[s] = __builtin_nontemporal_load(w + 4 * s);
   }
 
-  // 3. stage (and gather-copy) the activations, RMSNorm
-  float ss[8];
+  // 3. stage the activations in LDS
+  if (int(threadIdx.x) < NCH) {
 #pragma unroll
-  for (int b = 0; b < 8; ++b)
-    ss[b] = 0.f;
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int idx = int(threadIdx.x) + NT * i;
-    if (idx < B * NCH) {
-      const int b = idx / NCH, c = idx - b * NCH;
-      const u32x4 v = xr[i];
-      lds[b * ROWC + c] = v;
-      if (p.x_out && blockIdx.x == 0)
-        reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v;
-      if (p.norm_w) {
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        float t = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float lo = bflo(w4[q]), hi = bfhi(w4[q]);
-          t += lo * lo;
-          t += hi * hi;
-        }
-#pragma unroll
-        for (int bb = 0; bb < 8; ++bb)
-          ss[bb] += bb == b ? t : 0.f;
-      }
-    }
-  }
-  if (p.norm_w) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const float t = wave_sum(ss[b]);
-      if (lane == 0)
-        red_ss[b][wave] = t;
-    }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-      float total = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w)
-        total += red_ss[threadIdx.x][w];
-      scale_b[threadIdx.x] = rbf(1.0f / __builtin_sqrtf(total / float(K) + p.eps));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int idx = int(threadIdx.x) + NT * i;
-      if (idx < B * NCH) {
-        const int b = idx / NCH, c = idx - b * NCH;
-        const float scale = scale_b[b];
-        const u32x4 v = lds[b * ROWC + c], g = reinterpret_cast<const u32x4 *>(p.norm_w)[c];
-        const uint32_t vi[4] = {v.x, v.y, v.z, v.w}, gi[4] = {g.x, g.y, g.z, g.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t lo = f2bf(rbf(bflo(vi[q]) * scale) * bflo(gi[q]));
-          const uint32_t hi = f2bf(rbf(bfhi(vi[q]) * scale) * bfhi(gi[q]));
-          o[q] = lo | (hi << 16);
-        }
-        lds[b * ROWC + c] = u32x4{o[0], o[1], o[2], o[3]};
-      }
-    }
+    for (int b = 0; b < 8; ++b)
+      if (b < B)
+        lds[b * ROWC + c] = xr[b];
   }
   __syncthreads();
 
@@ -218,17 +211,30 @@ hipError_t launch_wk(const GemvParams &p, hipStream_t s) {
 bool gemv_mfma_supported(const GemvParams &p) {
   return p.batch >= 3 && p.batch <= 8 && (p.x_stride % 8 == 0 || p.embed) &&
          (p.k == 3072 || p.k == 8192 || p.k == 2048 || p.k == 6144) &&
-         (p.epilogue != kEpiSwiGLU || p.n % 2 == 0);
+         (p.epilogue != kEpiSwiGLU || p.n % 2 == 0) &&
+         (p.stage || (!p.norm_w && !p.embed && !p.x_out));
 }
 
 hipError_t launch_gemv_mfma(const GemvParams &p, hipStream_t s) {
   if (!gemv_mfma_supported(p) || p.n < 1)
     return hipErrorInvalidValue;
-  switch (p.k) {
-  case 3072: return launch_wk<4, 24>(p, s);   // 4 waves x 768 k
-  case 8192: return launch_wk<16, 16>(p, s);  // 16 waves x 512 k
-  case 2048: return launch_wk<4, 16>(p, s);
-  case 6144: return launch_wk<16, 12>(p, s);
+  GemvParams q = p;
+  if (p.norm_w || p.embed || p.x_out) {  // prepare the rows once
+    hipLaunchKernelGGL(stage_rows_kernel, dim3(p.batch), dim3(256), 0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      return e;
+    q.x = p.stage;
+    q.x_stride = p.k;
+    q.norm_w = nullptr;
+    q.embed = nullptr;
+    q.x_out = nullptr;
+  }
+  switch (q.k) {
+  case 3072: return launch_wk<8, 12>(q, s);   // 8 waves x 384 k (one column per thread)
+  case 8192: return launch_wk<16, 16>(q, s);  // 16 waves x 512 k
+  case 2048: return launch_wk<4, 16>(q, s);   // 4 waves x 512 k
+  case 6144: return launch_wk<16, 12>(q, s);  // 16 waves x 384 k
   }
   return hipErrorInvalidValue;
 }

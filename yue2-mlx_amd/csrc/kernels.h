@@ -31,6 +31,10 @@ struct GemvParams {
   int epilogue = kEpiStore;
   int seg0_start = 0, seg0_len = 1 << 30, seg1_start = 0;  // row map
   int32_t *advance = nullptr;  // block 0 increments advance[0..batch)
+  // [batch][k] scratch for the batched (MFMA) form: with a gather or an
+  // RMSNorm prologue, a row kernel first writes the prepared rows here once
+  // instead of every workgroup re-normalising them.
+  uint16_t *stage = nullptr;
 };
 hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
 // MFMA form for 3..8 independent rows (batched sequences); launch_gemv
