@@ -65,31 +65,38 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
 
   if (active) {
     const int last_cached = pos > 0 ? pos - 1 : 0;
-    // q/k/v inputs of this wave's heads (h = wave, wave + 4 < G + 2) first,
-    // then the first pass of K/V: the prologue waits only for the former
+    // q/k/v inputs of this wave's heads (h = wave, wave + 4 < G + 2) and
+    // their norm gains / RoPE rows first, then the first pass of K/V: the
+    // prologue waits only for the former (all loads branch-free)
     const uint16_t *row = p.qkv + size_t(b) * p.qkv_stride;
+    const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
+    const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
     uint32_t pair[2];
+    NormRope nr[2];
+    bool has_gain[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int h = min(wave + 4 * j, G + 1);
       const size_t col = h < G ? size_t(kvh * G + h) * D
                                : size_t(p.heads + (h - G) * Hkv + kvh) * D;
       pair[j] = reinterpret_cast<const uint32_t *>(row + col)[lane];
+      const uint16_t *gain = h < G ? p.q_norm : p.k_norm;
+      has_gain[j] = gain != nullptr;
+      load_rope(nr[j], cs, sn, lane);
+      load_gain(nr[j], has_gain[j] ? gain : cs, lane);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep the prologue inputs ahead of K/V
     u32x4 kr[8], vr[8];
     attn::load_k(kc, s0, wave, lane, last_cached, kr);
     attn::load_v(vc, s0, wave, lane, last_cached, vr);
 
     // ---- prologue: q heads, current k, current v ----
-    const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
-    const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
     const float qscale = scale * attn::kLog2e;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int h = wave + 4 * j;
       if (h < G + 2)
-        attn::prologue_head<G>(sh, h, pair[j], h < G ? p.q_norm : p.k_norm, p.eps, cs, sn,
-                               lane);
+        attn::prologue_head<G>(sh, h, pair[j], has_gain[j], p.eps, nr[j], lane);
     }
     __syncthreads();
     if (pos >= s0 && pos < s1 && threadIdx.x < D / 8 + D) {  // append (ar.cpp:119-123)
@@ -138,30 +145,38 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
   if (!is_last)
     return;
   const int n_active = (L + chunk - 1) / chunk;
-  // One memory round: thread x owns outputs (2 q, 2 q + 1), q = x + 256 r, and
-  // issues the 8-byte partial loads of all its splits up front (clamped to
-  // the active ones); meanwhile wave h turns the (m, l) of head h into merge
-  // weights, lane t for split t.
+  // One memory round: the (m, l) of all splits first (wave w: heads w and
+  // w + 4, lane t: split t), then thread x's 8-byte partials of outputs
+  // (2 q, 2 q + 1), q = x + 256 r, for up to kRound splits (clamped to the
+  // active ones); the merge weights are formed while the partials arrive.
   constexpr int kPairs = G * D / 2;
   constexpr int kRounds = (kPairs + 255) / 256;
+  constexpr int kRound = 32;
+  float mm[2], ll[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int h = min(wave + 4 * j, G - 1), t = min(lane, n_active - 1);
+    mm[j] = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
+    ll[j] = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);
+  }
   for (int r = 0; r < kRounds; ++r) {
     const int q = min(int(threadIdx.x) + 256 * r, kPairs - 1);
     const unsigned long long *po =
         reinterpret_cast<const unsigned long long *>(p.part_o + part * (G * D)) + q;
-    unsigned long long ov[kMaxSplits];
+    unsigned long long ov[kRound];
 #pragma unroll
-    for (int j = 0; j < kMaxSplits; ++j)
+    for (int j = 0; j < kRound; ++j)
       ov[j] = __hip_atomic_load(po + size_t(min(j, n_active - 1)) * (G * D / 2), __ATOMIC_RELAXED,
                                 __HIP_MEMORY_SCOPE_AGENT);
     if (r == 0) {
-      for (int h = wave; h < G; h += 4) {
-        const bool act = lane < n_active;
-        const int t = act ? lane : 0;
-        const float m = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
-        const float l = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);
-        const float w = merge_weight(m, l, act);
-        if (act)
-          s_w[lane][h] = w;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int h = wave + 4 * j;
+        if (h < G) {
+          const float w = merge_weight(mm[j], ll[j], lane < n_active);
+          if (lane < n_active)
+            s_w[lane][h] = w;
+        }
       }
       __syncthreads();
     }
@@ -169,13 +184,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
       const int h = (2 * q) / D;
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int j = 0; j < kMaxSplits; ++j) {
+      for (int j = 0; j < kRound; ++j) {
         if (j < n_active) {  // sequential over splits
           const float o0 = __builtin_bit_cast(float, uint32_t(ov[j]));
           const float o1 = __builtin_bit_cast(float, uint32_t(ov[j] >> 32));
           a0 = fmaf(s_w[j][h], o0, a0);
           a1 = fmaf(s_w[j][h], o1, a1);
         }
+      }
+      for (int j = kRound; j < n_active; ++j) {  // more splits than one round
+        const unsigned long long v = __hip_atomic_load(po + size_t(j) * (G * D / 2),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a0 = fmaf(s_w[j][h], __builtin_bit_cast(float, uint32_t(v)), a0);
+        a1 = fmaf(s_w[j][h], __builtin_bit_cast(float, uint32_t(v >> 32)), a1);
       }
       reinterpret_cast<uint32_t *>(p.out + size_t(b) * p.out_stride + size_t(kvh * G) * D)[q] =
           uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);

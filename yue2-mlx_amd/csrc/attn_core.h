@@ -92,14 +92,14 @@ __device__ __forceinline__ void load_v(const u32x4 *vc, int t0, int wave, int la
 
 // Prologue for head h of the workgroup (h < G: query head, h == G: key,
 // h == G + 1: value), one head per wave, lane l holding dims 2l and 2l + 1:
-// RMSNorm with the q/k gain and half-split RoPE (ar.cpp:268-277), then LDS.
-template <int G, class GainPtr>
-__device__ __forceinline__ void prologue_head(Lds<G> &sh, int h, uint32_t pair, GainPtr gain,
-                                              float eps, const uint16_t *cs, const uint16_t *sn,
-                                              int lane) {
+// RMSNorm with the q/k gain and half-split RoPE (ar.cpp:268-277; operands
+// preloaded in nr), then LDS.
+template <int G>
+__device__ __forceinline__ void prologue_head(Lds<G> &sh, int h, uint32_t pair, bool has_gain,
+                                              float eps, const NormRope &nr, int lane) {
   float y0 = bflo(pair), y1 = bfhi(pair);
   if (h <= G)
-    norm_rope_head(y0, y1, gain, eps, cs, sn, lane, y0, y1);
+    norm_rope_apply(y0, y1, has_gain, eps, nr, lane, y0, y1);
   const uint32_t packed = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
   if (h < G)
     reinterpret_cast<uint32_t *>(&sh.q[h][0])[lane] = packed;

@@ -221,33 +221,62 @@ __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
   return acc;
 }
 
-// q/k RMSNorm over a 128-wide head (ar.cpp:268-275, 30-35) followed by the
-// half-split RoPE (ar.cpp:52-87), one head per wave, lane l holding dims
-// 2l and 2l+1; cs/sn point at the bf16 cos/sin row of the position.
-// (GainPtr: a plain or an address-space-qualified pointer to the [D] gain.)
+// Per-lane operands of the q/k RMSNorm + RoPE of one head (lane l: dims 2l
+// and 2l + 1): the gain pair and the cos/sin pairs of its rotation index, so
+// that callers can issue these loads ahead of a larger stream.
+struct NormRope {
+  float g0 = 1.f, g1 = 1.f, c0, c1, s0, s1;
+};
+__device__ __forceinline__ void load_rope(NormRope &r, const uint16_t *cs, const uint16_t *sn,
+                                          int lane) {
+  const int j = (2 * lane) & 63;  // ar.cpp:52-87: pair (j, j + D/2)
+  const uint32_t c = reinterpret_cast<const uint32_t *>(cs)[j >> 1];
+  const uint32_t s = reinterpret_cast<const uint32_t *>(sn)[j >> 1];
+  r.c0 = bflo(c);
+  r.c1 = bfhi(c);
+  r.s0 = bflo(s);
+  r.s1 = bfhi(s);
+}
+template <class GainPtr>
+__device__ __forceinline__ void load_gain(NormRope &r, GainPtr gain, int lane) {
+  r.g0 = bf2f(gain[2 * lane]);
+  r.g1 = bf2f(gain[2 * lane + 1]);
+}
+
+// q/k RMSNorm over a 128-wide head (ar.cpp:268-275, 30-35; skipped without
+// a gain) followed by the half-split RoPE (ar.cpp:52-87), one head per wave,
+// lane l holding dims 2l and 2l+1; lanes l and l ^ 32 hold the partners.
+__device__ __forceinline__ void norm_rope_apply(float x0, float x1, bool has_gain, float eps,
+                                                const NormRope &r, int lane, float &y0,
+                                                float &y1) {
+  if (has_gain) {
+    const float ssq = wave_sum(x0 * x0 + x1 * x1);
+    const float scale = rbf(1.0f / __builtin_sqrtf(ssq / 128.0f + eps));
+    x0 = rbf(rbf(x0 * scale) * r.g0);
+    x1 = rbf(rbf(x1 * scale) * r.g1);
+  }
+  const float p0 = xor32(x0, lane), p1 = xor32(x1, lane);
+  if (lane < 32) {  // first half: first*c - second*s
+    y0 = rbf(rbf(x0 * r.c0) - rbf(p0 * r.s0));
+    y1 = rbf(rbf(x1 * r.c1) - rbf(p1 * r.s1));
+  } else {  // second half: second*c + first*s
+    y0 = rbf(rbf(x0 * r.c0) + rbf(p0 * r.s0));
+    y1 = rbf(rbf(x1 * r.c1) + rbf(p1 * r.s1));
+  }
+}
+
+// Both steps with the loads in place; cs/sn point at the bf16 cos/sin row of
+// the position. (GainPtr: a plain or an address-space-qualified pointer.)
 template <class GainPtr>
 __device__ __forceinline__ void norm_rope_head(float x0, float x1, GainPtr gain,
                                                float eps, const uint16_t *cs,
                                                const uint16_t *sn, int lane, float &y0,
                                                float &y1) {
-  if (gain) {  // ar.cpp:268-275 / ar.cpp:30-35 over D
-    const float ssq = wave_sum(x0 * x0 + x1 * x1);
-    const float scale = rbf(1.0f / __builtin_sqrtf(ssq / 128.0f + eps));
-    x0 = rbf(rbf(x0 * scale) * bf2f(gain[2 * lane]));
-    x1 = rbf(rbf(x1 * scale) * bf2f(gain[2 * lane + 1]));
-  }
-  // ar.cpp:52-87: pair (j, j + D/2); lanes l and l ^ 32 hold the partners.
-  const float p0 = xor32(x0, lane), p1 = xor32(x1, lane);
-  const int j = (2 * lane) & 63;
-  const float c0 = bf2f(cs[j]), c1 = bf2f(cs[j + 1]);
-  const float s0 = bf2f(sn[j]), s1 = bf2f(sn[j + 1]);
-  if (lane < 32) {  // first half: first*c - second*s
-    y0 = rbf(rbf(x0 * c0) - rbf(p0 * s0));
-    y1 = rbf(rbf(x1 * c1) - rbf(p1 * s1));
-  } else {  // second half: second*c + first*s
-    y0 = rbf(rbf(x0 * c0) + rbf(p0 * s0));
-    y1 = rbf(rbf(x1 * c1) + rbf(p1 * s1));
-  }
+  NormRope r;
+  load_rope(r, cs, sn, lane);
+  if (gain)
+    load_gain(r, gain, lane);
+  norm_rope_apply(x0, x1, bool(gain), eps, r, lane, y0, y1);
 }
 
 #endif

@@ -550,9 +550,13 @@ __device__ void attn_phase(SH &sh, const DecodeParams &p, const Ctx &cx, int l,
           if (wave_settled(fresh(pr.x, cx.tag) & fresh(pr.y, cx.tag), spin, cx))
             break;
         }
-        attn::prologue_head<G>(sh.at, h, (pr.x & 0xffffu) | (pr.y << 16),
-                               (const GLB uint16_t *)(h < G ? Lw.q_norm : Lw.k_norm), p.eps, cs,
-                               sn, lane);
+        const GLB uint16_t *gain = (const GLB uint16_t *)(h < G ? Lw.q_norm : Lw.k_norm);
+        NormRope nr;
+        load_rope(nr, cs, sn, lane);
+        if (gain)
+          load_gain(nr, gain, lane);
+        attn::prologue_head<G>(sh.at, h, (pr.x & 0xffffu) | (pr.y << 16), gain != nullptr,
+                               p.eps, nr, lane);
       }
       __syncthreads();
       if (pos >= s0 && pos < s1 && threadIdx.x < D / 8 + D) {  // append (ar.cpp:119-123)
