@@ -30,20 +30,18 @@ namespace {
 
 constexpr int D = attn::D;
 constexpr int kMaxSplits = 64;
-
-// s_waitcnt vmcnt(0): this wave's outstanding vector memory operations
-// (including stores) have completed. gfx9 encoding: vmcnt in bits [3:0] and
-// [15:14] (zero here), expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait).
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+constexpr int kWaves = 4;  // 128 keys per pass (8 waves measured no faster on MI355X)
 
 // Load coherent at device (agent) scope: served past any stale per-XCD L2 line.
 __device__ __forceinline__ float coherent_load(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, float scale) {
-  __shared__ attn::Lds<G> sh;
+template <int G, int W>
+__global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnDecodeParams p, float scale) {
+  constexpr int NT = 64 * W;
+  constexpr int kHeadsPerWave = (G + 2 + W - 1) / W;  // prologue heads (q heads, k, v)
+  __shared__ attn::Lds<G, W> sh;
   __shared__ float s_w[kMaxSplits][G];  // merge weights
   __shared__ int is_last;
 
@@ -65,18 +63,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
 
   if (active) {
     const int last_cached = pos > 0 ? pos - 1 : 0;
-    // q/k/v inputs of this wave's heads (h = wave, wave + 4 < G + 2) and
+    // q/k/v inputs of this wave's heads (h = wave + W j < G + 2) and
     // their norm gains / RoPE rows first, then the first pass of K/V: the
     // prologue waits only for the former (all loads branch-free)
     const uint16_t *row = p.qkv + size_t(b) * p.qkv_stride;
     const uint16_t *cs = p.rope_cos + size_t(pos) * (D / 2);
     const uint16_t *sn = p.rope_sin + size_t(pos) * (D / 2);
-    uint32_t pair[2];
-    NormRope nr[2];
-    bool has_gain[2];
+    uint32_t pair[kHeadsPerWave];
+    NormRope nr[kHeadsPerWave];
+    bool has_gain[kHeadsPerWave];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int h = min(wave + 4 * j, G + 1);
+    for (int j = 0; j < kHeadsPerWave; ++j) {
+      const int h = min(wave + W * j, G + 1);
       const size_t col = h < G ? size_t(kvh * G + h) * D
                                : size_t(p.heads + (h - G) * Hkv + kvh) * D;
       pair[j] = reinterpret_cast<const uint32_t *>(row + col)[lane];
@@ -93,8 +91,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
     // ---- prologue: q heads, current k, current v ----
     const float qscale = scale * attn::kLog2e;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int h = wave + 4 * j;
+    for (int j = 0; j < kHeadsPerWave; ++j) {
+      const int h = wave + W * j;
       if (h < G + 2)
         attn::prologue_head<G>(sh, h, pair[j], has_gain[j], p.eps, nr[j], lane);
     }
@@ -110,10 +108,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
       }
     }
 
-    // ---- passes over the split, then the 4-wave combine ----
+    // ---- passes over the split, then the W-wave combine ----
     attn::split<G>(sh, kc, vc, s0, s1, pos, last_cached, lane, wave, qscale, kr, vr);
     __syncthreads();
-    for (int e = threadIdx.x; e < G * D; e += 256) {
+    for (int e = threadIdx.x; e < G * D; e += NT) {
       float o, M, l;
       attn::combine<G>(sh, e, o, M, l);
       // write-through (agent-scope) stores: visible to every XCD once complete
@@ -145,22 +143,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
   if (!is_last)
     return;
   const int n_active = (L + chunk - 1) / chunk;
-  // One memory round: the (m, l) of all splits first (wave w: heads w and
-  // w + 4, lane t: split t), then thread x's 8-byte partials of outputs
-  // (2 q, 2 q + 1), q = x + 256 r, for up to kRound splits (clamped to the
-  // active ones); the merge weights are formed while the partials arrive.
+  // One memory round: the (m, l) of all splits first (wave w: heads w + W j,
+  // lane t: split t), then thread x's 8-byte partials of outputs (2 q,
+  // 2 q + 1), q = x + NT r, for up to kRound splits (clamped to the active
+  // ones); the merge weights are formed while the partials arrive.
   constexpr int kPairs = G * D / 2;
-  constexpr int kRounds = (kPairs + 255) / 256;
+  constexpr int kRounds = (kPairs + NT - 1) / NT;
   constexpr int kRound = 32;
-  float mm[2], ll[2];
+  constexpr int kMergeHeads = (G + W - 1) / W;
+  float mm[kMergeHeads], ll[kMergeHeads];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int h = min(wave + 4 * j, G - 1), t = min(lane, n_active - 1);
+  for (int j = 0; j < kMergeHeads; ++j) {
+    const int h = min(wave + W * j, G - 1), t = min(lane, n_active - 1);
     mm[j] = coherent_load(&p.part_ml[((part + t) * G + h) * 2]);
     ll[j] = coherent_load(&p.part_ml[((part + t) * G + h) * 2 + 1]);
   }
   for (int r = 0; r < kRounds; ++r) {
-    const int q = min(int(threadIdx.x) + 256 * r, kPairs - 1);
+    const int q = min(int(threadIdx.x) + NT * r, kPairs - 1);
     const unsigned long long *po =
         reinterpret_cast<const unsigned long long *>(p.part_o + part * (G * D)) + q;
     unsigned long long ov[kRound];
@@ -170,8 +169,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
                                 __HIP_MEMORY_SCOPE_AGENT);
     if (r == 0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int h = wave + 4 * j;
+      for (int j = 0; j < kMergeHeads; ++j) {
+        const int h = wave + W * j;
         if (h < G) {
           const float w = merge_weight(mm[j], ll[j], lane < n_active);
           if (lane < n_active)
@@ -180,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
       }
       __syncthreads();
     }
-    if (int(threadIdx.x) + 256 * r < kPairs) {
+    if (int(threadIdx.x) + NT * r < kPairs) {
       const int h = (2 * q) / D;
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
@@ -209,7 +208,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnDecodeParams p, fl
 template <int G>
 hipError_t launch_g(const AttnDecodeParams &p, hipStream_t s) {
   const float scale = float(std::pow(double(D), -0.5));  // ar.cpp:283
-  hipLaunchKernelGGL(attn_decode_kernel<G>, dim3(p.max_splits, p.kv_heads, p.batch), dim3(256), 0,
+  hipLaunchKernelGGL((attn_decode_kernel<G, kWaves>), dim3(p.max_splits, p.kv_heads, p.batch),
+                     dim3(64 * kWaves), 0,
                      s, p, scale);
   return hipGetLastError();
 }

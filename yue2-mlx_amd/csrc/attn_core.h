@@ -5,9 +5,9 @@
 // Reference: native/src/ar.cpp:268-291 (q/k RMSNorm, RoPE, SDPA with fp32
 // softmax and accumulation) and ar.cpp:88-91.
 //
-// A workgroup (4 waves) owns keys [s0, s1) of one kv head and the G <= 16
-// query heads sharing it. A pass covers kPass = 128 keys: wave w takes the
-// 32-key block t0 + 32 w. Both products run on v_mfma_f32_16x16x32_bf16 with
+// A workgroup (W waves) owns keys [s0, s1) of one kv head and the G <= 16
+// query heads sharing it. A pass covers 32 W keys: wave w takes the 32-key
+// block t0 + 32 w. Both products run on v_mfma_f32_16x16x32_bf16 with
 // the G heads as the 16 MFMA columns (columns >= G are zero):
 //
 //   S^T[key][head] = K[key][:] . q[head][:]   two 16-key tiles x 4 k-steps
@@ -33,7 +33,6 @@ namespace attn {
 
 constexpr int D = 128;
 constexpr int kBlock = 32;           // keys per V block = keys per wave per pass
-constexpr int kPass = 4 * kBlock;    // keys per workgroup pass
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -44,12 +43,12 @@ __host__ __device__ __forceinline__ size_t v_index(int t, int d) {
   return size_t(t >> 5) * (kBlock * D) + size_t(d) * kBlock + (t & (kBlock - 1));
 }
 
-template <int G>
+template <int G, int W = 4>
 struct Lds {
   u32x4 q[G][D / 8];        // normalised, rotated q heads (bf16, unscaled)
   u32x4 kv_new[2][D / 8];   // current key / value (bf16)
-  float w_m[4][G], w_l[4][G];
-  float w_o[4][G][D];
+  float w_m[W][G], w_l[W][G];
+  float w_o[W][G][D];
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -94,8 +93,8 @@ __device__ __forceinline__ void load_v(const u32x4 *vc, int t0, int wave, int la
 // h == G + 1: value), one head per wave, lane l holding dims 2l and 2l + 1:
 // RMSNorm with the q/k gain and half-split RoPE (ar.cpp:268-277; operands
 // preloaded in nr), then LDS.
-template <int G>
-__device__ __forceinline__ void prologue_head(Lds<G> &sh, int h, uint32_t pair, bool has_gain,
+template <int G, int W>
+__device__ __forceinline__ void prologue_head(Lds<G, W> &sh, int h, uint32_t pair, bool has_gain,
                                               float eps, const NormRope &nr, int lane) {
   float y0 = bflo(pair), y1 = bfhi(pair);
   if (h <= G)
@@ -117,13 +116,13 @@ __device__ __forceinline__ u32x4 with_elem(u32x4 v, int e, uint32_t val) {
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-// One pass over keys [t0, t0 + kPass) ∩ [s0, s1) with the online softmax
+// One pass over keys [t0, t0 + 32 W) ∩ [s0, s1) with the online softmax
 // state of this lane (head lane % 16): m, l (over this lane's keys), o (O^T
 // tiles: dims 16 dt + 4 (lane / 16) + [0, 4)). kr / vr hold the pass's
 // operands on entry; when `more`, the next pass's K rows are issued into kr
 // right after the S^T products and its V^T rows into vr after P.V.
-template <int G>
-__device__ __forceinline__ void pass(const Lds<G> &sh, const u32x4 *kc, const u32x4 *vc, int t0,
+template <int G, int W>
+__device__ __forceinline__ void pass(const Lds<G, W> &sh, const u32x4 *kc, const u32x4 *vc, int t0,
                                      int s1, int pos, int last_cached, bool more, int wave,
                                      int lane, const u32x4 (&qb)[4], float qscale,
                                      u32x4 (&kr)[8], u32x4 (&vr)[8], float &m_run, float &l_run,
@@ -146,7 +145,7 @@ __device__ __forceinline__ void pass(const Lds<G> &sh, const u32x4 *kc, const u3
       st[T] = mfma(kr[4 * T + s], qb[s], st[T]);
   }
   if (more)
-    load_k(kc, t0 + kPass, wave, lane, last_cached, kr);
+    load_k(kc, t0 + kBlock * W, wave, lane, last_cached, kr);
   // the current key's values (dim 16 dt + i) into element pos - (blk0 + 8 r)
   const int ep = pos - (blk0 + 8 * r);
   if (ep >= 0 && ep < 8) {
@@ -196,14 +195,14 @@ __device__ __forceinline__ void pass(const Lds<G> &sh, const u32x4 *kc, const u3
       o[dt] = mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[dt]);
   }
   if (more)
-    load_v(vc, t0 + kPass, wave, lane, last_cached, vr);
+    load_v(vc, t0 + kBlock * W, wave, lane, last_cached, vr);
 }
 
 // All passes of [s0, s1) for this wave (s0 a multiple of 32), starting from
 // kr / vr holding the first pass; leaves the wave's (m, l, o) in LDS (w_m,
 // w_l, w_o). Needs the prologue's q in LDS (after a barrier).
-template <int G>
-__device__ __forceinline__ void split(Lds<G> &sh, const u32x4 *kc, const u32x4 *vc, int s0,
+template <int G, int W>
+__device__ __forceinline__ void split(Lds<G, W> &sh, const u32x4 *kc, const u32x4 *vc, int s0,
                                       int s1, int pos, int last_cached, int lane, int wave,
                                       float qscale, u32x4 (&kr)[8], u32x4 (&vr)[8]) {
   const int r = lane >> 4, i = lane & 15;
@@ -218,9 +217,9 @@ __device__ __forceinline__ void split(Lds<G> &sh, const u32x4 *kc, const u32x4 *
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
     o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int t0 = s0;; t0 += kPass) {
-    const bool more = t0 + kPass < s1;  // uniform
-    pass<G>(sh, kc, vc, t0, s1, pos, last_cached, more, wave, lane, qb, qscale, kr, vr, m_run,
+  for (int t0 = s0;; t0 += kBlock * W) {
+    const bool more = t0 + kBlock * W < s1;  // uniform
+    pass<G, W>(sh, kc, vc, t0, s1, pos, last_cached, more, wave, lane, qb, qscale, kr, vr, m_run,
             l_run, o);
     if (!more)
       break;
@@ -237,17 +236,20 @@ __device__ __forceinline__ void split(Lds<G> &sh, const u32x4 *kc, const u32x4 *
   }
 }
 
-// Combine the four waves for element e = h * D + d of the split partial
+// Combine the W waves for element e = h * D + d of the split partial
 // (after a barrier): running max M, weighted o and l.
-template <int G>
-__device__ __forceinline__ void combine(const Lds<G> &sh, int e, float &o, float &M,
+template <int G, int W>
+__device__ __forceinline__ void combine(const Lds<G, W> &sh, int e, float &o, float &M,
                                         float &lsum) {
   const int h = e / D, d = e % D;
-  M = fmaxf(fmaxf(sh.w_m[0][h], sh.w_m[1][h]), fmaxf(sh.w_m[2][h], sh.w_m[3][h]));
+  M = sh.w_m[0][h];
+#pragma unroll
+  for (int w = 1; w < W; ++w)
+    M = fmaxf(M, sh.w_m[w][h]);
   o = 0.f;
   lsum = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < W; ++w) {
     const float f =
         sh.w_m[w][h] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sh.w_m[w][h] - M);
     o = fmaf(f, sh.w_o[w][h][d], o);

@@ -221,6 +221,11 @@ __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
   return acc;
 }
 
+// s_waitcnt vmcnt(0): this wave's outstanding vector memory operations
+// (including stores) have completed. gfx9 encoding: vmcnt in bits [3:0] and
+// [15:14] (zero here), expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 (no wait).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Per-lane operands of the q/k RMSNorm + RoPE of one head (lane l: dims 2l
 // and 2l + 1): the gain pair and the cos/sin pairs of its rotation index, so
 // that callers can issue these loads ahead of a larger stream.
