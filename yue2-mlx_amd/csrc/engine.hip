@@ -228,6 +228,8 @@ size_t align_elems(size_t n) { return (n + 127) & ~size_t(127); }  // 256 B
 
 struct LayerW {
   uint16_t *input_ln, *post_ln, *q_norm, *k_norm, *qkv, *o, *gu, *down;
+  // MFMA-tiled copies of the projections for batched decode (launch_tile_rows)
+  uint16_t *qkv_t = nullptr, *o_t = nullptr, *gu_t = nullptr, *down_t = nullptr;
 };
 
 struct PhaseInfo {
@@ -289,12 +291,18 @@ struct yuear_engine {
   uint16_t *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
   std::vector<LayerW> layers;
   uint16_t *rope_cos = nullptr, *rope_sin = nullptr;
+  // MFMA-tiled projection copies, built by the first session of 3+ branches
+  // (6.15 GB more at the 3B shape: HBM is plentiful, the batched GEMVs read
+  // 1 KiB contiguous per wave-load from them)
+  uint16_t *tiled = nullptr, *lm_head_t = nullptr;
+  std::mutex tiled_mu;
   std::atomic<bool> cancelled{false};
   std::mutex busy;
 
   ~yuear_engine() {
     if (weights) (void)hipFree(weights);
     if (rope_cos) (void)hipFree(rope_cos);
+    if (tiled) (void)hipFree(tiled);
   }
   void check_cancelled(const char *where) {
     if (cancelled.load(std::memory_order_relaxed))
@@ -506,6 +514,42 @@ void build_engine(yuear_engine &E, const yuear_weight_source *src) {
   upload(E.rope_sin, sn.data(), sn.size());
 }
 
+// MFMA-tiled copies of every projection and the lm_head, for the batched
+// (3..8 sequence) GEMVs; only for the K values that form has instances.
+bool mfma_shapes(const Config &c) {
+  auto ok = [](int k) { return k == 2048 || k == 3072 || k == 6144 || k == 8192; };
+  return ok(c.H) && ok(c.Hq * c.D) && ok(c.F);
+}
+void build_tiled(yuear_engine &E, hipStream_t st) {
+  std::lock_guard<std::mutex> lock(E.tiled_mu);
+  const Config &c = E.cfg;
+  if (E.tiled || !mfma_shapes(c))
+    return;
+  auto tiled_elems = [](size_t n, size_t k) { return align_elems((n + 15) / 16 * 16 * k); };
+  const size_t H = c.H, F = c.F, QD = size_t(c.Hq) * c.D, KD = size_t(c.Hkv) * c.D;
+  const size_t per_layer = tiled_elems(QD + 2 * KD, H) + tiled_elems(H, QD) +
+                           tiled_elems(2 * F, H) + tiled_elems(H, F);
+  const size_t total = per_layer * c.layers + tiled_elems(c.V, H);
+  uint16_t *base = nullptr;
+  HIPC(hipMalloc(&base, total * 2));
+  uint16_t *cur = base;
+  auto tile = [&](const uint16_t *w, size_t n, size_t k) {
+    uint16_t *out = cur;
+    cur += tiled_elems(n, k);
+    HIPC(launch_tile_rows(w, int(n), int(k), out, st));
+    return out;
+  };
+  for (auto &L : E.layers) {
+    L.qkv_t = tile(L.qkv, QD + 2 * KD, H);
+    L.o_t = tile(L.o, H, QD);
+    L.gu_t = tile(L.gu, 2 * F, H);
+    L.down_t = tile(L.down, H, F);
+  }
+  E.lm_head_t = tile(E.lm_head, c.V, H);
+  HIPC(hipStreamSynchronize(st));
+  E.tiled = base;
+}
+
 // ---------------------------------------------------------------------------
 // session
 void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity,
@@ -523,6 +567,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.phase = phase_info(phase, c.V);
   HIPC(hipSetDevice(E->device));
   HIPC(hipStreamCreateWithFlags(&S.stream, hipStreamNonBlocking));
+  if (branches >= 3)
+    build_tiled(*E, S.stream);
   const size_t kv = size_t(c.layers) * branches * c.Hkv * size_t(S.kv_stride) * c.D;
   S.kc = S.alloc<uint16_t>(kv);
   S.vc = S.alloc<uint16_t>(kv);
@@ -657,6 +703,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   q.norm_w = L.input_ln;
   q.eps = c.eps;
   q.stage = S.stage;
+  q.w_tiled = L.qkv_t;
   q.y = S.qkv;
   q.y_stride = c.qkv();
   HIPC(launch_gemv(q, st));
@@ -695,6 +742,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   o.y = S.x;
   o.y_stride = c.H;
   o.epilogue = kEpiResidual;
+  o.w_tiled = L.o_t;
   HIPC(launch_gemv(o, st));
 
   GemvParams g;
@@ -707,6 +755,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   g.norm_w = L.post_ln;
   g.eps = c.eps;
   g.stage = S.stage;
+  g.w_tiled = L.gu_t;
   g.y = S.act;
   g.y_stride = c.F;
   g.epilogue = kEpiSwiGLU;
@@ -722,6 +771,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   d.y = S.x;
   d.y_stride = c.H;
   d.epilogue = kEpiResidual;
+  d.w_tiled = L.down_t;
   HIPC(launch_gemv(d, st));
 }
 
@@ -741,6 +791,7 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   h.norm_w = E.final_norm;
   h.eps = c.eps;
   h.stage = batch <= S.B ? S.stage : nullptr;
+  h.w_tiled = E.lm_head_t;
   h.y = out;
   h.y_stride = S.phase.stride();
   h.seg0_start = S.phase.seg0_start;
@@ -762,16 +813,17 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
   if (which == "qkv") {
     g.w = L.qkv; g.n = c.qkv(); g.k = c.H; g.x = S.x; g.x_stride = c.H;
     g.norm_w = L.input_ln; g.y = S.qkv; g.y_stride = c.qkv(); g.stage = S.stage;
+    g.w_tiled = L.qkv_t;
   } else if (which == "o_proj") {
     g.w = L.o; g.n = c.H; g.k = c.Hq * c.D; g.x = S.attn; g.x_stride = c.Hq * c.D;
-    g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual;
+    g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual; g.w_tiled = L.o_t;
   } else if (which == "gate_up") {
     g.w = L.gu; g.n = 2 * c.F; g.k = c.H; g.x = S.x; g.x_stride = c.H;
     g.norm_w = L.post_ln; g.y = S.act; g.y_stride = c.F; g.epilogue = kEpiSwiGLU;
-    g.stage = S.stage;
+    g.stage = S.stage; g.w_tiled = L.gu_t;
   } else if (which == "down") {
     g.w = L.down; g.n = c.H; g.k = c.F; g.x = S.act; g.x_stride = c.F;
-    g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual;
+    g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual; g.w_tiled = L.down_t;
   } else if (which == "lm_head") {
     enqueue_head(S, S.x, S.B, c.H, S.logits, nullptr);
     return;

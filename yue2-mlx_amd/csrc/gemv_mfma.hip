@@ -41,6 +41,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 // rounding points of ar.cpp:30-35, written to p.stage.
 __global__ __launch_bounds__(256) void stage_rows_kernel(GemvParams p) {
   __shared__ float red[4];
+  constexpr int kMaxChunks = 4;  // k <= 8192
   const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = p.k >> 3;
   const uint16_t *src;
@@ -51,17 +52,25 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(GemvParams p) {
     src = p.x + size_t(b) * p.x_stride;
   }
   const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src);
+  const u32x4 *g4 = reinterpret_cast<const u32x4 *>(p.norm_w ? p.norm_w : src);
   u32x4 *dst = reinterpret_cast<u32x4 *>(p.stage + size_t(b) * p.k);
+  // one round of loads: this thread's chunks c = t + 256 i and their gains
+  u32x4 v[kMaxChunks], g[kMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = min(int(threadIdx.x) + 256 * i, nch - 1);
+    v[i] = s4[c];
+    g[i] = g4[c];
+  }
   float ss = 0.f;
-  for (int c = threadIdx.x; c < nch; c += 256) {
-    const u32x4 v = s4[c];
-    if (p.x_out)
-      reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v;
-    if (!p.norm_w) {
-      dst[c] = v;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c >= nch)
       continue;
-    }
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    if (p.x_out)
+      reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v[i];
+    const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float lo = bflo(w4[q]), hi = bfhi(w4[q]);
@@ -69,18 +78,28 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(GemvParams p) {
       ss += hi * hi;
     }
   }
-  if (!p.norm_w)
+  if (!p.norm_w) {
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      if (c < nch)
+        dst[c] = v[i];
+    }
     return;
+  }
   ss = wave_sum(ss);
   if (lane == 0)
     red[wave] = ss;
   __syncthreads();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float scale = rbf(1.0f / __builtin_sqrtf(total / float(p.k) + p.eps));
-  const u32x4 *g4 = reinterpret_cast<const u32x4 *>(p.norm_w);
-  for (int c = threadIdx.x; c < nch; c += 256) {
-    const u32x4 v = s4[c], g = g4[c];
-    const uint32_t vi[4] = {v.x, v.y, v.z, v.w}, gi[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c >= nch)
+      continue;
+    const uint32_t vi[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    const uint32_t gi[4] = {g[i].x, g[i].y, g[i].z, g[i].w};
     uint32_t o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -117,16 +136,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. this wave's weight stream: row n0 + l % 16 (clamped; mapped for the
-  // lm_head phases), k = wave * KW + 32 s + 8 (l / 16)
+  // lm_head phases), k = wave * KW + 32 s + 8 (l / 16); from the tiled copy
+  // when there is one (the 16-byte piece of (row, k-step) sits at
+  // ((row / 16) (K / 32) + k-step) 64 + row % 16 + 16 (l / 16))
   u32x4 a[KSTEPS];
   {
     const int lr = min(n0 + (lane & 15), p.n - 1);
     const int row = lr < p.seg0_len ? p.seg0_start + lr : p.seg1_start + (lr - p.seg0_len);
+    const bool tiled = p.w_tiled != nullptr;
     const u32x4 *w =
-        reinterpret_cast<const u32x4 *>(p.w + size_t(row) * K) + wave * (KSTEPS * 4) + (lane >> 4);
+        tiled ? reinterpret_cast<const u32x4 *>(p.w_tiled) +
+                    (size_t(row >> 4) * (K / 32) + wave * KSTEPS) * 64 + (row & 15) + 16 * (lane >> 4)
+              : reinterpret_cast<const u32x4 *>(p.w + size_t(row) * K) + wave * (KSTEPS * 4) +
+                    (lane >> 4);
+    const int step = tiled ? 64 : 4;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s)
-      a[s] = __builtin_nontemporal_load(w + 4 * s);
+      a[s] = __builtin_nontemporal_load(w + step * s);
   }
 
   // 3. stage the activations in LDS
@@ -206,7 +232,33 @@ hipError_t launch_wk(const GemvParams &p, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+__global__ __launch_bounds__(256) void tile_rows_kernel(const uint16_t *w, int n, int k,
+                                                        uint16_t *out, size_t total) {
+  const size_t o = size_t(blockIdx.x) * 256 + threadIdx.x;  // 16-byte piece of out
+  if (o >= total)
+    return;
+  const int l = int(o & 63);
+  const size_t blk = o >> 6;
+  const int ks = k / 32;
+  const size_t t = blk / ks;
+  const int s = int(blk % ks);
+  const size_t row = t * 16 + (l & 15);
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (row < size_t(n))
+    v = reinterpret_cast<const u32x4 *>(w + row * k + 32 * s + 8 * (l >> 4))[0];
+  reinterpret_cast<u32x4 *>(out)[o] = v;
+}
+
 }  // namespace
+
+hipError_t launch_tile_rows(const uint16_t *w, int n, int k, uint16_t *out, hipStream_t s) {
+  if (n < 1 || k < 32 || k % 32)
+    return hipErrorInvalidValue;
+  const size_t total = size_t((n + 15) / 16) * (k / 32) * 64;
+  hipLaunchKernelGGL(tile_rows_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, w, n,
+                     k, out, total);
+  return hipGetLastError();
+}
 
 bool gemv_mfma_supported(const GemvParams &p) {
   return p.batch >= 3 && p.batch <= 8 && (p.x_stride % 8 == 0 || p.embed) &&

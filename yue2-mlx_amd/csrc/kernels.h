@@ -35,12 +35,21 @@ struct GemvParams {
   // RMSNorm prologue, a row kernel first writes the prepared rows here once
   // instead of every workgroup re-normalising them.
   uint16_t *stage = nullptr;
+  // The same weight rows in the MFMA-tiled layout of launch_tile_rows, read
+  // by the batched form when given (1 KiB contiguous per wave-load instead of
+  // 16 row pieces of 64 bytes).
+  const uint16_t *w_tiled = nullptr;
 };
 hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
 // MFMA form for 3..8 independent rows (batched sequences); launch_gemv
 // dispatches to it when gemv_mfma_supported(p).
 bool gemv_mfma_supported(const GemvParams &p);
 hipError_t launch_gemv_mfma(const GemvParams &p, hipStream_t s);
+// Copy W [n][k] (k a multiple of 32) into the MFMA-tiled layout: for each
+// 16-row tile t and 32-column step s, 1 KiB whose 16-byte piece l is row
+// 16 t + l % 16, columns 32 s + 8 (l / 16) + [0, 8) (rows past n zero);
+// out holds ceil(n / 16) * 16 * k elements.
+hipError_t launch_tile_rows(const uint16_t *w, int n, int k, uint16_t *out, hipStream_t s);
 
 // KV cache layout of one (branch, kv head), `capacity` slots (a multiple of
 // 32): K row-major [capacity][128]; V in 32-slot blocks stored dim-major,
