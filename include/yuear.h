@@ -216,7 +216,9 @@ int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,
                       const uint16_t *dev_norm_w, float eps, uint16_t *dev_y,
                       int32_t y_stride, int32_t epilogue, void *stream);
 /* Fused decode attention of one layer (see yuear_session_begin layout):
- * qkv [batch][(Hq+2Hkv)*128], caches [batch][Hkv][cap][128], pos [batch],
+ * qkv [batch][(Hq+2Hkv)*128], caches [batch][Hkv] x cap slots (cap a
+ * multiple of 32; K row-major [cap][128], V in 32-slot blocks stored
+ * dim-major, element (t, d) at (t/32)*4096 + d*32 + t%32), pos [batch],
  * rope tables [positions][64], out [batch][Hq*128]. */
 int32_t yuear_op_attention_decode(
     const uint16_t *dev_qkv, const uint16_t *dev_q_norm,
@@ -228,7 +230,9 @@ int32_t yuear_op_attention_decode(
 int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                       int32_t ldc, int32_t residual, void *stream);
-/* Causal fp32-opmath attention for T queries at positions pos0 + t. */
+/* Causal fp32-opmath attention for T queries at positions pos0 + t over one
+ * branch's caches ([Hkv] x cap slots, the layout of
+ * yuear_op_attention_decode). */
 int32_t yuear_op_attention_prefill(const uint16_t *dev_q,
                                    const uint16_t *dev_k_cache,
                                    const uint16_t *dev_v_cache, int32_t tokens,
