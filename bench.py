@@ -265,8 +265,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-launches", type=int, default=112)
-    ap.add_argument("--decode", choices=("persistent", "kernels"), default="kernels",
-                    help="decode step as one persistent kernel or one kernel per op")
+    ap.add_argument("--decode", choices=("kernels", "fused", "persistent"), default="kernels",
+                    help="decode step: one kernel per op, a fused QKV+attention+o_proj "
+                         "launch per layer, or one persistent kernel")
     ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8"), default="decode",
                     help="workload (decode: the headline batch-1 KV-4096 line)")
     ap.add_argument("--phase-trace", action="store_true",

@@ -156,12 +156,16 @@ yuear_status yuear_session_set_position(yuear_session *session, int32_t branch,
 /* Decode-step execution: YUEAR_DECODE_KERNELS replays one kernel per op
  * (QKV, attention, O, gate/up, down per layer, lm_head); YUEAR_DECODE_PERSISTENT
  * runs the whole step as one persistent kernel (hidden sizes 3072/2048 with
- * 8 kv heads, 1 or 2 branches). Both produce the same bits. Replaces the
- * per-op graph of GraphAR (cuda_graph.py:43-240) with one launch per token.
- * The default is YUEAR_DECODE_KERNELS unless YUEAR_DECODE=persistent is set
- * in the environment when the session begins. */
+ * 8 kv heads, 1 or 2 branches); YUEAR_DECODE_FUSED runs QKV + attention +
+ * o_proj of a layer as one launch (1 or 2 branches, query heads per kv head
+ * 2-4, hidden 256/2048/3072 equal to heads x 128), then gate/up and down.
+ * All produce the same bits. They replace the per-op graph of GraphAR
+ * (cuda_graph.py:43-240). The default is YUEAR_DECODE_KERNELS (the fastest
+ * measured on MI355X); YUEAR_DECODE=persistent|fused in the environment
+ * when the session begins selects another where available. */
 #define YUEAR_DECODE_KERNELS 0
 #define YUEAR_DECODE_PERSISTENT 1
+#define YUEAR_DECODE_FUSED 2
 yuear_status yuear_session_set_decode_path(yuear_session *session, int32_t path,
                                            char **error_json);
 int32_t yuear_session_decode_path(const yuear_session *session);

@@ -1,5 +1,5 @@
-"""Persistent decode step (one launch per token) against the per-op decode
-kernels on the GPU.
+"""Persistent decode step (one launch per token) and the fused QKV +
+attention + o_proj layer launch against the per-op decode kernels on the GPU.
 
 The persistent kernel repeats the per-op kernels' arithmetic operation for
 operation, so the two paths must agree bit for bit: logits of every step,
@@ -77,6 +77,85 @@ def test_persistent_step_matches_per_op_kernels_bitwise(engine, branches, capaci
     assert np.isfinite(a[0].view(np.uint16).astype(np.float32)).all()
 
 
+@pytest.mark.parametrize("branches,capacity,lengths,n_steps", [
+    (1, 64, [5], 6),
+    (1, 20, [1], 18),           # one split; fills the cache to its last slot
+    (2, 700, [513, 200], 4),    # ragged branches
+    (1, 4200, [4090], 3),       # 33 splits around KV 4096
+])
+def test_fused_layer_matches_per_op_kernels_bitwise(engine, branches, capacity, lengths,
+                                                    n_steps):
+    rng = np.random.default_rng(capacity + 7 * branches)
+    V = engine.config["vocab_size"]
+    prompts = [rng.integers(0, V, size=n).tolist() for n in lengths]
+    steps = [rng.integers(0, V, size=branches).tolist() for _ in range(n_steps)]
+    assert_same(run(engine, "kernels", branches, capacity, prompts, steps),
+                run(engine, "fused", branches, capacity, prompts, steps))
+
+
+@pytest.mark.parametrize("config", ["tiny", "hidden_2048"])
+def test_fused_layer_other_shapes(yuear_lib, config):
+    from conftest import TINY
+    cfg = {"tiny": TINY, "hidden_2048": HIDDEN_2048}[config]
+    e = yuear_lib.Engine(cfg, None, seed=21)
+    try:
+        V = cfg["vocab_size"]
+        rng = np.random.default_rng(6)
+        prompts = [rng.integers(0, V, size=n).tolist() for n in (9, 4)]
+        steps = [rng.integers(0, V, size=2).tolist() for _ in range(5)]
+        cap = min(64, cfg["max_position_embeddings"])
+        assert_same(run(e, "kernels", 2, cap, prompts, steps), run(e, "fused", 2, cap, prompts, steps))
+        assert_same(run(e, "kernels", 1, cap, prompts[:1], [s[:1] for s in steps]),
+                    run(e, "fused", 1, cap, prompts[:1], [s[:1] for s in steps]))
+    finally:
+        e.close()
+
+
+def test_fused_path_after_persistent_steps(engine):
+    # Steps of the persistent path do not advance the fused path's step
+    # counter; switching back must not let words of the last fused step pass
+    # for fresh ones. Interleave the paths and compare with the per-op path.
+    rng = np.random.default_rng(14)
+    prompt = rng.integers(0, 83968, size=21).tolist()
+    toks = rng.integers(0, 83968, size=6).tolist()
+    ref = engine.session(1, 64)
+    ref.decode_path = "kernels"
+    ref.prefill(0, prompt)
+    want = [ref.step(t) for t in toks]
+    ref.close()
+    s = engine.session(1, 64)
+    s.decode_path = "fused"
+    s.prefill(0, prompt)
+    got = []
+    for i, t in enumerate(toks):
+        s.decode_path = ("fused", "persistent")[i % 2]
+        got.append(s.step(t))
+    s.close()
+    np.testing.assert_array_equal(np.stack(got), np.stack(want))
+
+
+def test_fused_expired_wait_is_reported(engine, monkeypatch):
+    # A wait bound of 0 makes every wait that is not satisfied on its first
+    # read give up (o_proj workgroups start while the attention still runs);
+    # the kernel runs to its end and the host reports the expired wait.
+    monkeypatch.setenv("YUEAR_FUSED_WAIT_US", "0")
+    s = engine.session(1, 32)
+    s.decode_path = "fused"
+    s.prefill(0, [1, 2, 3])
+    with pytest.raises(RuntimeError, match="dependency wait expired"):
+        s.step(4)
+    s.close()
+    monkeypatch.delenv("YUEAR_FUSED_WAIT_US")
+    a = engine.session(1, 32)
+    a.decode_path = "fused"
+    a.prefill(0, [1, 2, 3])
+    b = engine.session(1, 32)
+    b.prefill(0, [1, 2, 3])
+    np.testing.assert_array_equal(a.step(4), b.step(4))
+    a.close()
+    b.close()
+
+
 def test_semantic_phase_odd_row_count(yuear_lib):
     e = yuear_lib.Engine(TWO_LAYER_NATIVE, None, seed=5)
     try:
@@ -111,6 +190,12 @@ def test_unsupported_shape_keeps_per_op_path(yuear_lib):
         assert s.decode_path == "kernels"
         with pytest.raises(ValueError, match="persistent decode step is not available"):
             s.decode_path = "persistent"
+        s.decode_path = "fused"
+        s.close()
+        s = e.session(3, 16)  # more than two branches: per-op kernels
+        assert s.decode_path == "kernels"
+        with pytest.raises(ValueError, match="fused decode layer is not available"):
+            s.decode_path = "fused"
         s.close()
     finally:
         e.close()
@@ -127,7 +212,7 @@ def test_device_loop_tokens_agree(engine, sampling):
     rng = np.random.default_rng(8)
     prompt = rng.integers(0, 83968, size=77).tolist()
     out = {}
-    for path in ("kernels", "persistent"):
+    for path in ("kernels", "persistent", "fused"):
         s = engine.session(1, 256)
         s.decode_path = path
         last = s.prefill(0, prompt)
@@ -135,9 +220,10 @@ def test_device_loop_tokens_agree(engine, sampling):
         out[path] = (tokens, s.position(0), s.read_kv(1, 0, s.position(0)))
         s.close()
         assert ms > 0 and last.shape == (83968,)
-    assert out["kernels"][0] == out["persistent"][0]
-    assert out["kernels"][1] == out["persistent"][1]
-    np.testing.assert_array_equal(out["kernels"][2][0], out["persistent"][2][0])
+    for path in ("persistent", "fused"):
+        assert out["kernels"][0] == out[path][0]
+        assert out["kernels"][1] == out[path][1]
+        np.testing.assert_array_equal(out["kernels"][2][0], out[path][2][0])
 
 
 def test_generate_tokens_on_persistent_path(engine, monkeypatch):

@@ -278,7 +278,7 @@ struct yuear_session {
   uint16_t *pin_logits = nullptr;
   std::vector<void *> allocations;
   // persistent decode step (decode.hip): one launch per token
-  int decode_path = 0;  // YUEAR_DECODE_KERNELS or YUEAR_DECODE_PERSISTENT
+  int decode_path = 0;  // YUEAR_DECODE_KERNELS, _PERSISTENT or _FUSED
   int decode_grid = 0;  // co-resident workgroups; 0: shape not supported
   int decode_spins = 1 << 20;  // bounded-wait polls (YUEAR_DECODE_SPIN_LIMIT)
   int32_t *dsync = nullptr;     // counters + error word, zero between launches
@@ -287,6 +287,14 @@ struct yuear_session {
   uint32_t *dxs = nullptr, *dqkv = nullptr, *dattn = nullptr, *dact = nullptr;
   uint32_t *dpart_o = nullptr, *dpart_ml = nullptr;
   int32_t *pin_err = nullptr;
+  // fused QKV + attention + o_proj layer kernel (fused.hip): per-layer
+  // activation words, the step counter that tags them (advanced by the
+  // lm_head) and the sticky error word of its bounded waits
+  bool fused_ok = false;
+  uint32_t *fqkv = nullptr, *fattn = nullptr;
+  u32x4 *fpart = nullptr;
+  int32_t *fsync = nullptr;  // [0] step counter, [1] error word
+  long long fused_ticks = 2000000;  // 20 ms per wait (YUEAR_FUSED_WAIT_US)
   hipGraphExec_t step_exec = nullptr;
   hipGraph_t step_graph = nullptr;
   hipGraphExec_t gen_exec = nullptr;  // sampler + step, for timed loops
@@ -604,9 +612,29 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
     S.dlayers = S.alloc<DecodeLayer>(c.layers);
     HIPC(hipMemcpyAsync(S.dlayers, table.data(), table.size() * sizeof(DecodeLayer),
                         hipMemcpyHostToDevice, S.stream));
-    const char *env = std::getenv("YUEAR_DECODE");
-    S.decode_path = env && std::string(env) == "persistent" ? YUEAR_DECODE_PERSISTENT
-                                                            : YUEAR_DECODE_KERNELS;
+  }
+  // fused layer kernel (1-2 branches)
+  S.fused_ok = fused_layer_supported(c.H, c.Hq, c.Hkv, c.D, branches);
+  if (S.fused_ok) {
+    const size_t words = size_t(c.layers) * branches * (c.qkv() + c.Hq * c.D);
+    S.fqkv = S.alloc<uint32_t>(words);  // zero words carry tag 0, which no step uses
+    S.fattn = S.fqkv + size_t(c.layers) * branches * c.qkv();
+    HIPC(hipMemsetAsync(S.fqkv, 0, words * 4, S.stream));
+    S.fsync = S.alloc<int32_t>(2);
+    HIPC(hipMemsetAsync(S.fsync, 0, 8, S.stream));
+    const size_t pv = size_t(branches) * c.Hkv * S.max_splits * (G * (c.D / 2) + G);
+    S.fpart = S.alloc<u32x4>(pv);  // zero: tag 0, which no launch uses
+    HIPC(hipMemsetAsync(S.fpart, 0, pv * 16, S.stream));
+    if (const char *env = std::getenv("YUEAR_FUSED_WAIT_US"))
+      S.fused_ticks = std::max(1LL, std::atoll(env)) * 100;
+  }
+  S.decode_path = YUEAR_DECODE_KERNELS;
+  if (const char *env = std::getenv("YUEAR_DECODE")) {
+    const std::string v = env;
+    if (v == "persistent" && S.dsync)
+      S.decode_path = YUEAR_DECODE_PERSISTENT;
+    else if (v == "fused" && S.fused_ok)
+      S.decode_path = YUEAR_DECODE_FUSED;
   }
   HIPC(hipStreamSynchronize(S.stream));
 }
@@ -619,11 +647,19 @@ void set_device_pos(yuear_session &S) {
 }
 
 // decode kernels of one layer on S.x (all branches)
+void enqueue_fused_qkv_attn_o(yuear_session &S, int l, bool embed_first);
+void enqueue_ffn(yuear_session &S, int l);
+
 void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   yuear_engine &E = *S.e;
   const Config &c = E.cfg;
   const LayerW &L = E.layers[l];
   hipStream_t st = S.stream;
+  if (S.decode_path == YUEAR_DECODE_FUSED) {
+    enqueue_fused_qkv_attn_o(S, l, embed_first);
+    enqueue_ffn(S, l);
+    return;
+  }
   GemvParams q;
   q.w = L.qkv;
   q.n = c.qkv();
@@ -682,6 +718,15 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   o.w_tiled = L.o_t;
   HIPC(launch_gemv(o, st));
 
+  enqueue_ffn(S, l);
+}
+
+// post-attention RMSNorm + gate/up + SwiGLU, down + residual (ar.cpp:295-298)
+void enqueue_ffn(yuear_session &S, int l) {
+  yuear_engine &E = *S.e;
+  const Config &c = E.cfg;
+  const LayerW &L = E.layers[l];
+  hipStream_t st = S.stream;
   GemvParams g;
   g.w = L.gu;
   g.n = 2 * c.F;
@@ -712,6 +757,69 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   HIPC(launch_gemv(d, st));
 }
 
+// QKV + attention + o_proj of layer l as one launch (fused.hip)
+void enqueue_fused_qkv_attn_o(yuear_session &S, int l, bool embed_first) {
+  yuear_engine &E = *S.e;
+  const Config &c = E.cfg;
+  const LayerW &L = E.layers[l];
+  FusedLayerParams f;
+  GemvParams &q = f.q;
+  q.w = L.qkv;
+  q.n = c.qkv();
+  q.k = c.H;
+  q.batch = S.B;
+  q.x = S.x;
+  q.x_stride = c.H;
+  if (embed_first) {
+    q.embed = E.embed;
+    q.tokens = S.tok;
+    q.embed_rows = c.V;
+  }
+  q.norm_w = L.input_ln;
+  q.eps = c.eps;
+  q.y_stride = c.qkv();
+  AttnDecodeParams &a = f.a;
+  a.q_norm = c.qk_norm ? L.q_norm : nullptr;
+  a.k_norm = c.qk_norm ? L.k_norm : nullptr;
+  a.eps = c.eps;
+  a.rope_cos = E.rope_cos;
+  a.rope_sin = E.rope_sin;
+  a.k_cache = S.kc + S.layer_kv_offset(l, 0);
+  a.v_cache = S.vc + S.layer_kv_offset(l, 0);
+  a.pos = S.pos;
+  a.heads = c.Hq;
+  a.kv_heads = c.Hkv;
+  a.head_dim = c.D;
+  a.capacity = S.kv_stride;
+  a.batch = S.B;
+  a.max_splits = S.max_splits;
+  a.part_o = S.part_o;
+  a.part_ml = S.part_ml;
+  a.counters = S.counters;
+  GemvParams &o = f.o;
+  o.w = L.o;
+  o.n = c.H;
+  o.k = c.Hq * c.D;
+  o.batch = S.B;
+  o.x_stride = c.Hq * c.D;
+  o.y = S.x;
+  o.y_stride = c.H;
+  o.epilogue = kEpiResidual;
+  if (embed_first) {  // the residual stream of the first layer is the embedding row
+    o.embed = E.embed;
+    o.tokens = S.tok;
+    o.embed_rows = c.V;
+  }
+  f.qkv_words = S.fqkv + size_t(l) * S.B * c.qkv();
+  f.attn_words = S.fattn + size_t(l) * S.B * c.Hq * c.D;
+  f.part = S.fpart;
+  f.layer = l;
+  f.epoch = S.fsync;
+  f.err = S.fsync + 1;
+  f.max_ticks = S.fused_ticks;
+  HIPC(launch_fused_layer(f, S.stream));
+}
+
 void enqueue_one(yuear_session &S, const std::string &which, int l);
 
 void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, uint16_t *out,
@@ -735,6 +843,8 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   h.seg0_len = S.phase.seg0_len;
   h.seg1_start = S.phase.seg1_start;
   h.advance = advance;
+  if (advance)  // a decode step: the step counter that tags the fused path's words
+    h.epoch = S.fsync;
   HIPC(launch_gemv(h, S.stream));
 }
 
@@ -832,10 +942,20 @@ void ensure_step_graph(yuear_session &S) {
   HIPC(hipGraphInstantiate(&S.step_exec, S.step_graph, nullptr, nullptr, 0));
 }
 
-// The persistent step reports an expired dependency wait through a sticky
-// word (its workgroups were not all resident): the results since the last
-// check are invalid. Synchronises the session stream.
+// The persistent step and the fused layer kernel report an expired dependency
+// wait through a sticky word: the results since the last check are invalid.
+// Synchronises the session stream.
 void check_decode(yuear_session &S) {
+  if (S.fsync) {
+    HIPC(hipMemcpyAsync(S.pin_err, S.fsync + 1, 4, hipMemcpyDeviceToHost, S.stream));
+    HIPC(hipStreamSynchronize(S.stream));
+    if (*S.pin_err != 0) {
+      HIPC(hipMemsetAsync(S.fsync + 1, 0, 4, S.stream));
+      HIPC(hipStreamSynchronize(S.stream));
+      throw Error("RuntimeError",
+                  "fused decode layer: a dependency wait expired; the decoded state is invalid");
+    }
+  }
   if (!S.dsync)
     return;
   HIPC(hipMemcpyAsync(S.pin_err, S.dsync + kSyncError, 4, hipMemcpyDeviceToHost, S.stream));
@@ -1225,12 +1345,24 @@ yuear_status yuear_session_set_position(yuear_session *S, int32_t branch, int32_
 
 yuear_status yuear_session_set_decode_path(yuear_session *S, int32_t path, char **error_json) {
   return guarded(error_json, [&] {
-    if (!S || (path != YUEAR_DECODE_KERNELS && path != YUEAR_DECODE_PERSISTENT))
-      invalid("decode path must be YUEAR_DECODE_KERNELS or YUEAR_DECODE_PERSISTENT");
+    if (!S || (path != YUEAR_DECODE_KERNELS && path != YUEAR_DECODE_PERSISTENT &&
+               path != YUEAR_DECODE_FUSED))
+      invalid("decode path must be YUEAR_DECODE_KERNELS, YUEAR_DECODE_PERSISTENT or "
+              "YUEAR_DECODE_FUSED");
     if (path == YUEAR_DECODE_PERSISTENT && !S->dsync)
       invalid("the persistent decode step is not available for this model shape / branch count");
+    if (path == YUEAR_DECODE_FUSED && !S->fused_ok)
+      invalid("the fused decode layer is not available for this model shape / branch count");
     if (path != S->decode_path) {
       drop_graphs(*S);
+      if (path == YUEAR_DECODE_FUSED) {
+        // steps of the persistent path do not advance the step counter: move
+        // it on so that no word of an earlier fused step carries the next tag
+        int32_t epoch = 0;
+        HIPC(hipMemcpy(&epoch, S->fsync, 4, hipMemcpyDeviceToHost));
+        epoch += 1;
+        HIPC(hipMemcpy(S->fsync, &epoch, 4, hipMemcpyHostToDevice));
+      }
       S->decode_path = path;
     }
   });

@@ -117,7 +117,7 @@ for _name, (_res, _args) in _SIGS.items():
     _fn.restype, _fn.argtypes = _res, _args
 
 EXPORTS = tuple(_SIGS)
-DECODE_PATHS = ("kernels", "persistent")  # YUEAR_DECODE_KERNELS, YUEAR_DECODE_PERSISTENT
+DECODE_PATHS = ("kernels", "persistent", "fused")  # YUEAR_DECODE_KERNELS, _PERSISTENT, _FUSED
 
 
 def _take_error(err):
