@@ -27,8 +27,7 @@ template <int G>
 hipError_t launch_g(const AttnDecodeParams &p, hipStream_t s) {
   const float scale = float(std::pow(double(D), -0.5));  // ar.cpp:283
   hipLaunchKernelGGL((attn_decode_kernel<G, kWaves>), dim3(p.max_splits, p.kv_heads, p.batch),
-                     dim3(64 * kWaves), 0,
-                     s, p, scale);
+                     dim3(64 * kWaves), 0, s, p, scale);
   return hipGetLastError();
 }
 

@@ -17,11 +17,13 @@
 // arrive on a kv head (device-scope counter) merges the splits exactly.
 //
 // WORDS: q/k/v are activation words of the same launch (gemv_core.h), re-read
-// until fresh while the first K/V pass is in flight; the split partials are
-// stored tagged (io.tag32) without a counter, and the workgroup of split 0
-// re-reads them until fresh, merges in the same order and stores the output
-// as activation words. Otherwise plain bf16 rows in and out with the counter
-// merge.
+// until fresh while the first K/V pass is in flight, and the output is stored
+// as activation words; otherwise plain bf16 rows in and out.
+// TAGGED (implied by WORDS): the split partials are stored tagged (io.tag32,
+// unique per step and layer) without waiting, and the workgroup of split 0
+// re-reads them until fresh and merges in the same order as the counter
+// merge; otherwise partials are followed by a store-completion wait and a
+// device-scope counter whose last arrival merges.
 #pragma once
 #include "attn_core.h"
 #include "common.h"
@@ -75,25 +77,27 @@ __device__ __forceinline__ float part_hi(u32x4 v) {
 }
 
 // Merge of the n_active tagged partials of (b, kv head) by one workgroup,
-// the same arithmetic and order as the counter-based merge below: the (m, l)
-// of all splits are re-read until fresh, then each thread's output pairs over
-// the splits in order, kRound splits per memory round.
-template <int G, int W>
+// the same arithmetic and order as the counter-based merge below. One memory
+// round: the (m, l) of all splits (wave w: heads w + W j, lane t: split t)
+// and this thread's output pairs of the first kRound splits are re-read
+// together until every vector is fresh; further splits (more than kRound) are
+// read afterwards. Output: activation words (WORDS) or bf16 pairs at p.out.
+template <int G, int W, bool WORDS>
 __device__ __forceinline__ void merge_tagged(const AttnDecodeParams &p, int b, int kvh,
                                              size_t part, int n_active, AttnShared<G, W> &sm,
                                              const WordIO &io) {
   constexpr int D = attn::D, NT = 64 * W;
   constexpr int kPairs = G * D / 2;
   constexpr int kRounds = (kPairs + NT - 1) / NT;
-  constexpr int kRound = 24;
+  constexpr int kRound = kRounds == 1 ? 24 : 12;  // splits per memory round (registers)
   constexpr int kMergeHeads = (G + W - 1) / W;
   constexpr int kVecs = part_vecs<G>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const u32x4 *pt = io.part + part * kVecs;
   const auto rp = word_rsrc(pt, uint32_t(n_active * kVecs) * 16);
   const long long t0 = __builtin_amdgcn_s_memrealtime();
-  // (m, l): wave w heads w + W j, lane t split t
   float mm[kMergeHeads], ll[kMergeHeads];
+  u32x4 ov[kRounds][kRound];
   for (;;) {
     bool ok = true;
 #pragma unroll
@@ -103,6 +107,15 @@ __device__ __forceinline__ void merge_tagged(const AttnDecodeParams &p, int b, i
       ok = ok && part_fresh(v, io.tag32);
       mm[j] = part_lo(v);
       ll[j] = part_hi(v);
+    }
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int q = min(int(threadIdx.x) + NT * r, kPairs - 1);
+#pragma unroll
+      for (int j = 0; j < kRound; ++j) {
+        ov[r][j] = word_load4(rp, uint32_t(min(j, n_active - 1) * kVecs + q) * 16);
+        ok = ok && part_fresh(ov[r][j], io.tag32);
+      }
     }
     if (__syncthreads_and(ok))
       break;
@@ -122,47 +135,47 @@ __device__ __forceinline__ void merge_tagged(const AttnDecodeParams &p, int b, i
     }
   }
   __syncthreads();
+#pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     const int q = min(int(threadIdx.x) + NT * r, kPairs - 1);
     const int h = (2 * q) / D;
     float a0 = 0.f, a1 = 0.f;
-    for (int j0 = 0; j0 < n_active; j0 += kRound) {
-      u32x4 ov[kRound];
-      for (;;) {
-        bool ok = true;
 #pragma unroll
-        for (int j = 0; j < kRound; ++j) {
-          ov[j] = word_load4(rp, uint32_t(min(j0 + j, n_active - 1) * kVecs + q) * 16);
-          ok = ok && part_fresh(ov[j], io.tag32);
-        }
-        if (__syncthreads_and(ok))
-          break;
-        const bool give_up = threadIdx.x == 0 && wait_expired(io, t0);
-        if (__syncthreads_or(give_up))
+    for (int j = 0; j < kRound; ++j) {
+      if (j < n_active) {  // sequential over splits
+        a0 = fmaf(sm.s_w[j][h], part_lo(ov[r][j]), a0);
+        a1 = fmaf(sm.s_w[j][h], part_hi(ov[r][j]), a1);
+      }
+    }
+    for (int j = kRound; j < n_active; ++j) {  // more splits than one round
+      u32x4 v;
+      for (;;) {
+        v = word_load4(rp, uint32_t(j * kVecs + q) * 16);
+        if (part_fresh(v, io.tag32) || wait_expired(io, t0))
           break;
         __builtin_amdgcn_s_sleep(1);
       }
-#pragma unroll
-      for (int j = 0; j < kRound; ++j) {
-        if (j0 + j < n_active) {  // sequential over splits
-          a0 = fmaf(sm.s_w[j0 + j][h], part_lo(ov[j]), a0);
-          a1 = fmaf(sm.s_w[j0 + j][h], part_hi(ov[j]), a1);
-        }
-      }
+      a0 = fmaf(sm.s_w[j][h], part_lo(v), a0);
+      a1 = fmaf(sm.s_w[j][h], part_hi(v), a1);
     }
     if (int(threadIdx.x) + NT * r < kPairs) {
-      const unsigned long long w2 =
-          (static_cast<unsigned long long>((io.tag << 16) | f2bf(a1)) << 32) |
-          ((io.tag << 16) | f2bf(a0));
-      __hip_atomic_store(reinterpret_cast<unsigned long long *>(
-                             io.out + size_t(b) * io.out_stride + size_t(kvh * G) * D) + q,
-                         w2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (WORDS) {
+        const unsigned long long w2 =
+            (static_cast<unsigned long long>((io.tag << 16) | f2bf(a1)) << 32) |
+            ((io.tag << 16) | f2bf(a0));
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(
+                               io.out + size_t(b) * io.out_stride + size_t(kvh * G) * D) + q,
+                           w2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        reinterpret_cast<uint32_t *>(p.out + size_t(b) * p.out_stride + size_t(kvh * G) * D)[q] =
+            uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);
+      }
     }
   }
   stamp_ready(io, 2);
 }
 
-template <int G, int W, bool WORDS>
+template <int G, int W, bool WORDS, bool TAGGED = WORDS>
 __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scale, int s, int kvh,
                                            int b, int nsplit, AttnShared<G, W> &sm,
                                            const WordIO &io) {
@@ -268,7 +281,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
     // ---- passes over the split, then the W-wave combine ----
     attn::split<G>(sh, kc, vc, s0, s1, pos, last_cached, lane, wave, qscale, kr, vr);
     __syncthreads();
-    if constexpr (WORDS) {
+    if constexpr (TAGGED) {
       stamp_ready(io, 3);
       // tagged partials {tag, o0, tag, o1} per output pair and {tag, m, tag, l}
       // per head, stored without waiting: the merger re-reads until fresh
@@ -315,10 +328,10 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
       }
     }
   }
-  if constexpr (WORDS) {
+  if constexpr (TAGGED) {
     stamp_ready(io, 4);
     if (s == 0)
-      merge_tagged<G, W>(p, b, kvh, part, (L + chunk - 1) / chunk, sm, io);
+      merge_tagged<G, W, WORDS>(p, b, kvh, part, (L + chunk - 1) / chunk, sm, io);
     return;
   }
 

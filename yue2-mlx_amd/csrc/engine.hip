@@ -613,6 +613,18 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
     HIPC(hipMemcpyAsync(S.dlayers, table.data(), table.size() * sizeof(DecodeLayer),
                         hipMemcpyHostToDevice, S.stream));
   }
+  // step counter (advanced by the lm_head of every decode step) and the
+  // sticky error word of the fused path's bounded waits; its tagged split
+  // partials of the attention (counter-free merge), shared by all layers
+  S.fsync = S.alloc<int32_t>(2);
+  HIPC(hipMemsetAsync(S.fsync, 0, 8, S.stream));
+  {
+    const size_t pv = size_t(branches) * c.Hkv * S.max_splits * (G * (c.D / 2) + G);
+    S.fpart = S.alloc<u32x4>(pv);  // zero: tag 0, which no launch uses
+    HIPC(hipMemsetAsync(S.fpart, 0, pv * 16, S.stream));
+  }
+  if (const char *env = std::getenv("YUEAR_FUSED_WAIT_US"))
+    S.fused_ticks = std::max(0LL, std::atoll(env)) * 100;
   // fused layer kernel (1-2 branches)
   S.fused_ok = fused_layer_supported(c.H, c.Hq, c.Hkv, c.D, branches);
   if (S.fused_ok) {
@@ -620,13 +632,6 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
     S.fqkv = S.alloc<uint32_t>(words);  // zero words carry tag 0, which no step uses
     S.fattn = S.fqkv + size_t(c.layers) * branches * c.qkv();
     HIPC(hipMemsetAsync(S.fqkv, 0, words * 4, S.stream));
-    S.fsync = S.alloc<int32_t>(2);
-    HIPC(hipMemsetAsync(S.fsync, 0, 8, S.stream));
-    const size_t pv = size_t(branches) * c.Hkv * S.max_splits * (G * (c.D / 2) + G);
-    S.fpart = S.alloc<u32x4>(pv);  // zero: tag 0, which no launch uses
-    HIPC(hipMemsetAsync(S.fpart, 0, pv * 16, S.stream));
-    if (const char *env = std::getenv("YUEAR_FUSED_WAIT_US"))
-      S.fused_ticks = std::max(1LL, std::atoll(env)) * 100;
   }
   S.decode_path = YUEAR_DECODE_KERNELS;
   if (const char *env = std::getenv("YUEAR_DECODE")) {
@@ -953,7 +958,7 @@ void check_decode(yuear_session &S) {
       HIPC(hipMemsetAsync(S.fsync + 1, 0, 4, S.stream));
       HIPC(hipStreamSynchronize(S.stream));
       throw Error("RuntimeError",
-                  "fused decode layer: a dependency wait expired; the decoded state is invalid");
+                  "decode step: a dependency wait expired; the decoded state is invalid");
     }
   }
   if (!S.dsync)
@@ -1355,14 +1360,12 @@ yuear_status yuear_session_set_decode_path(yuear_session *S, int32_t path, char 
       invalid("the fused decode layer is not available for this model shape / branch count");
     if (path != S->decode_path) {
       drop_graphs(*S);
-      if (path == YUEAR_DECODE_FUSED) {
-        // steps of the persistent path do not advance the step counter: move
-        // it on so that no word of an earlier fused step carries the next tag
-        int32_t epoch = 0;
-        HIPC(hipMemcpy(&epoch, S->fsync, 4, hipMemcpyDeviceToHost));
-        epoch += 1;
-        HIPC(hipMemcpy(S->fsync, &epoch, 4, hipMemcpyHostToDevice));
-      }
+      // steps of the persistent path do not advance the step counter: move
+      // it on so that no word or partial of an earlier step carries the next tag
+      int32_t epoch = 0;
+      HIPC(hipMemcpy(&epoch, S->fsync, 4, hipMemcpyDeviceToHost));
+      epoch += 1;
+      HIPC(hipMemcpy(S->fsync, &epoch, 4, hipMemcpyHostToDevice));
       S->decode_path = path;
     }
   });
