@@ -48,6 +48,12 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 
+// Rows per wave of the two GEMV roles: two (one row per wave, the per-op
+// choice at batch 1, measured 4% slower here: the launch's register budget,
+// set by the attention role, limits residency, and more workgroups queue).
+template <int B>
+constexpr int fused_rows() { return 2; }
+
 template <int B, int G, int KC>
 __global__ __launch_bounds__(256) void fused_layer_kernel(FusedLayerParams fp) {
   extern __shared__ u32x4 xs[];  // [B][k / 8] GEMV activation chunks
@@ -74,7 +80,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedLayerParams fp) {
     role = 0;
     io.out = fp.qkv_words;
     io.out_stride = fp.q.y_stride;
-    gemv_block<B, KC, 2, kEpiStore, kGemvProduce>(fp.q, blk, xs, red, io);
+    gemv_block<B, KC, fused_rows<B>(), kEpiStore, kGemvProduce>(fp.q, blk, xs, red, io);
   } else if ((blk -= fp.qkv_blocks) < fp.attn_blocks) {
     role = 1;
     const int splits = fp.a.max_splits, hkv = fp.a.kv_heads;
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void fused_layer_kernel(FusedLayerParams fp) {
     io.late_weights = fp.o_late != 0;
     io.in = fp.attn_words;
     io.in_stride = fp.o.x_stride;
-    gemv_block<B, KC, 2, kEpiResidual, kGemvConsume>(fp.o, blk, xs, red, io);
+    gemv_block<B, KC, fused_rows<B>(), kEpiResidual, kGemvConsume>(fp.o, blk, xs, red, io);
   }
   if (tr && threadIdx.x == 0) {
     uint32_t xcc, hw;
@@ -152,9 +158,10 @@ hipError_t launch_fused_layer(FusedLayerParams p, hipStream_t s) {
       !p.qkv_words || !p.attn_words || !p.part || p.o.batch != p.q.batch ||
       p.a.batch != p.q.batch)
     return hipErrorInvalidValue;
-  p.qkv_blocks = p.q.n / 8;  // 4 waves x 2 rows
+  const int rows = 4 * (p.q.batch == 1 ? fused_rows<1>() : fused_rows<2>());  // per workgroup
+  p.qkv_blocks = p.q.n / rows;
   p.attn_blocks = p.a.max_splits * p.a.kv_heads * p.a.batch;
-  p.o_blocks = p.o.n / 8;
+  p.o_blocks = p.o.n / rows;
   p.scale = float(std::pow(double(attn::D), -0.5));  // ar.cpp:283
   if (p.q.batch == 1) return launch_b<1>(p, s);
   return launch_b<2>(p, s);
