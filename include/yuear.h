@@ -87,6 +87,22 @@ yuear_status yuear_engine_create(const yuear_model_config *config,
                                  const yuear_weight_source *weights,
                                  yuear_engine **out, char **error_json);
 void yuear_engine_destroy(yuear_engine *engine);
+/* Checkpoint directory (replaces ARModel(directory, precision, verify=false),
+ * ar.cpp:133-238): conversion.json (schema 1; precisions[precision].ar =
+ * "ar-<precision>.safetensors", bf16 with dtype "bfloat16"), config.json
+ * (ar.cpp:161-192 checks; strict != 0 also requires the YuE2 dimensions of
+ * ar.cpp:164-178, otherwise any architecture this build implements), then
+ * the safetensors file: every tensor of ar.cpp:216-233 with its shape and
+ * BF16 dtype and nothing else, with the reference's error messages.
+ * precision "8bit"/"4bit" manifests are validated, then refused (bf16
+ * weights only). Errors: FileNotFoundError (status 1) for missing files or
+ * precisions, ValueError (status 2) otherwise. inspect reads and checks the
+ * directory without touching the GPU and returns the architecture. */
+yuear_status yuear_checkpoint_inspect(const char *directory, const char *precision,
+                                      int32_t strict, yuear_model_config *config_out,
+                                      char **error_json);
+yuear_status yuear_engine_load(const char *directory, const char *precision, int32_t strict,
+                               yuear_engine **out, char **error_json);
 /* Thread-safe cooperative cancellation of the running call (lyra.h:40). */
 void yuear_engine_cancel(yuear_engine *engine);
 /* Deterministic weight generator (host): the bytes RANDOM sources upload. */

@@ -62,6 +62,10 @@ _SIGS = {
     "yuear_engine_create": (C.c_int, [_P(ModelConfig), _P(WeightSource), _P(C.c_void_p),
                                       _P(C.c_void_p)]),
     "yuear_engine_destroy": (None, [C.c_void_p]),
+    "yuear_checkpoint_inspect": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int32, _P(ModelConfig),
+                                           _P(C.c_void_p)]),
+    "yuear_engine_load": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int32, _P(C.c_void_p),
+                                    _P(C.c_void_p)]),
     "yuear_engine_cancel": (None, [C.c_void_p]),
     "yuear_tensor_id": (C.c_int32, [C.c_char_p]),
     "yuear_random_tensor": (None, [C.c_uint64, C.c_int32, C.c_float, C.c_float, C.c_int64,
@@ -135,8 +139,8 @@ def _check(status, err):
     if status == 0:
         return
     info = _take_error(err)
-    kind = {"ValueError": ValueError, "InterruptedError": InterruptedError}.get(info.get("type"),
-                                                                              RuntimeError)
+    kind = {"ValueError": ValueError, "InterruptedError": InterruptedError,
+            "FileNotFoundError": FileNotFoundError}.get(info.get("type"), RuntimeError)
     if status == 130:
         kind = InterruptedError
     raise kind(info.get("message", ""))
@@ -257,6 +261,22 @@ def _i32(seq):
     return np.ascontiguousarray(arr.astype(np.int32))
 
 
+def inspect_checkpoint(directory, precision="bf16", strict=False):
+    """Validate a converted checkpoint directory without the GPU; returns its
+    architecture as a config dict."""
+    cfg = ModelConfig()
+    err = C.c_void_p()
+    _check(lib.yuear_checkpoint_inspect(os.fsencode(directory), precision.encode(), int(strict),
+                                        C.byref(cfg), C.byref(err)), err)
+    return dict(hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                num_hidden_layers=cfg.num_hidden_layers,
+                num_attention_heads=cfg.num_attention_heads,
+                num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                vocab_size=cfg.vocab_size, max_position_embeddings=cfg.max_position_embeddings,
+                rms_norm_eps=float(cfg.rms_norm_eps), rope_theta=float(cfg.rope_theta),
+                qk_norm=bool(cfg.qk_norm))
+
+
 class Engine:
     """ARModel equivalent: device weights for one config (ar.cpp:133-245)."""
 
@@ -280,6 +300,21 @@ class Engine:
         _check(lib.yuear_engine_create(C.byref(self._cfg), C.byref(src), C.byref(handle),
                                        C.byref(err)), err)
         self.handle = handle
+
+    @classmethod
+    def load(cls, directory, precision="bf16", strict=False):
+        """ARModel(directory, precision) (ar.cpp:133-238) from a converted
+        checkpoint directory (conversion.json, config.json,
+        ar-<precision>.safetensors)."""
+        self = cls.__new__(cls)
+        self.config = inspect_checkpoint(directory, precision, strict)
+        self._cfg = _config_struct(self.config)
+        handle = C.c_void_p()
+        err = C.c_void_p()
+        _check(lib.yuear_engine_load(os.fsencode(directory), precision.encode(), int(strict),
+                                     C.byref(handle), C.byref(err)), err)
+        self.handle = handle
+        return self
 
     def close(self):
         if getattr(self, "handle", None):
