@@ -46,25 +46,37 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def weight_bytes(c):
+def bytes_per_weight(bits):
+    """HBM bytes per linear weight: bf16, or affine group-64 codes plus one
+    bf16 scale and one bf16 bias per 64 weights."""
+    return 2.0 if not bits else bits / 8 + 4 / 64
+
+
+def precision_bits(args):
+    return {"bf16": 0, "8bit": 8, "4bit": 4}[args.precision]
+
+
+def weight_bytes(c, bits=0):
     H, F, V, L = c["hidden_size"], c["intermediate_size"], c["vocab_size"], c["num_hidden_layers"]
     qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
     per_layer = (qd + 2 * kd) * H + H * qd + 2 * F * H + H * F  # linear weights
-    return 2 * (L * per_layer + V * H)  # + lm_head (the embedding row gather is 6 KiB)
+    # + lm_head (the embedding row gather is 6 KiB)
+    return int(bytes_per_weight(bits) * (L * per_layer + V * H))
 
 
-def kernel_bytes(c, kernel, kv_len):
+def kernel_bytes(c, kernel, kv_len, bits=0):
     """Algorithmic HBM bytes of one launch (weights + activations + KV)."""
     H, F, V = c["hidden_size"], c["intermediate_size"], c["vocab_size"]
     qd, kd = c["num_attention_heads"] * 128, c["num_key_value_heads"] * 128
-    return {
-        "qkv": 2 * ((qd + 2 * kd) * H + H + (qd + 2 * kd)),
+    w = bytes_per_weight(bits)
+    return int({
+        "qkv": w * (qd + 2 * kd) * H + 2 * (H + (qd + 2 * kd)),
         "attention": kv_len * 2 * kd * 2 + 2 * (qd + 2 * kd + qd) + 2 * 2 * kd,
-        "o_proj": 2 * (H * qd + qd + 2 * H),
-        "gate_up": 2 * (2 * F * H + H + F),
-        "down": 2 * (H * F + F + 2 * H),
-        "lm_head": 2 * (V * H + H + V),
-    }[kernel]
+        "o_proj": w * H * qd + 2 * (qd + 2 * H),
+        "gate_up": w * 2 * F * H + 2 * (H + F),
+        "down": w * H * F + 2 * (F + 2 * H),
+        "lm_head": w * V * H + 2 * (H + V),
+    }[kernel])
 
 
 def gemv_shape(c, kernel):
@@ -114,7 +126,7 @@ def run_cfg(args, engine, c):
     decode_s = timing["seconds"] - timing["prefill_seconds"]
     tps = (len(tokens) - 1) / decode_s
     L = 512 + len(tokens) / 2  # mean per-branch KV length
-    step_bytes = weight_bytes(c) + 2 * L * KV_BYTES_PER_POS
+    step_bytes = weight_bytes(c, precision_bits(args)) + 2 * L * KV_BYTES_PER_POS
     log(f"[bench] cfg: {len(tokens)} tokens, prefill {timing['prefill_seconds']:.3f}s, "
         f"decode {tps:.1f} tok/s")
     return {"metric": "CFG decode tokens/sec (batch 2 cond+uncond, scale 1.5, top-k 50 / "
@@ -183,7 +195,7 @@ def run_batch8(args, engine, c):
     wall = time.perf_counter() - t
     agg = B * steps / wall
     mean_kv = float(np.mean(lens)) + 8 + steps / 2
-    step_bytes = weight_bytes(c) + B * mean_kv * KV_BYTES_PER_POS
+    step_bytes = weight_bytes(c, precision_bits(args)) + B * mean_kv * KV_BYTES_PER_POS
     # per-kernel device time at batch 8; the projections run on MFMA
     # (v_mfma_f32_16x16x32_bf16, 8 of 16 columns live), so their MFMA
     # utilisation is the useful flops over the dense bf16 peak
@@ -261,6 +273,9 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--kv", type=int, default=4096)
+    ap.add_argument("--precision", choices=("bf16", "8bit", "4bit"), default="bf16",
+                    help="linear weights: bf16 (the headline metric) or affine group-64 "
+                         "quantized (the reference's 8bit / 4bit checkpoints)")
     ap.add_argument("--seed", type=int, default=20251201)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -299,10 +314,13 @@ def main():
 
     t_start = time.perf_counter()
     c = CONFIG
+    bits = precision_bits(args)
     log(f"[bench] generating 3B weights on host ({weight_bytes(c) / 1e9:.2f} GB) ...")
     weights = yuear.random_weights(c, args.seed)
+    if bits:
+        weights = yuear.quantized_weights(weights, bits)
     log(f"[bench] weights ready {time.perf_counter() - t_start:.1f}s; uploading")
-    engine = yuear.Engine(c, weights)
+    engine = yuear.Engine(c, weights, bits=bits)
     if args.config != "decode":
         line = {"cfg": run_cfg, "long": run_long, "batch8": run_batch8}[args.config](
             args, engine, c)
@@ -345,7 +363,7 @@ def main():
     ms_per_step = 1e3 * wall / K
     value = K / wall
     mean_kv = prefill + W + (K - 1) / 2 + 1
-    step_bytes = weight_bytes(c) + mean_kv * KV_BYTES_PER_POS
+    step_bytes = weight_bytes(c, bits) + mean_kv * KV_BYTES_PER_POS
     log(f"[bench] decode {K} steps: {ms_per_step:.4f} ms/token wall, {dev_ms:.4f} ms device, "
         f"{value:.1f} tok/s, step roofline {step_bytes / (ms_per_step / 1e3) / PEAK_HBM:.3f}")
 
@@ -354,7 +372,7 @@ def main():
     for name in ("qkv", "attention", "o_proj", "gate_up", "down", "lm_head"):
         launches = args.kernel_launches if name != "lm_head" else max(8, args.kernel_launches // 8)
         ms = session.time_kernel(name, launches)
-        nbytes = kernel_bytes(c, name, session.position(0) + 1)
+        nbytes = kernel_bytes(c, name, session.position(0) + 1, bits)
         kernels[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
                          "GBps": round(nbytes / (ms / 1e3) / 1e9, 1)}
         log(f"[bench] {name:9s} {ms * 1e3:8.2f} us  {nbytes / 1e6:8.2f} MB  "
@@ -364,7 +382,7 @@ def main():
         # read at the current length (+ activations, < 0.01 %)
         ms = session.time_kernel("decode_step", step_launches)
         kv_now = session.position(0) + 1
-        nbytes = weight_bytes(c) + kv_now * KV_BYTES_PER_POS
+        nbytes = weight_bytes(c, bits) + kv_now * KV_BYTES_PER_POS
         achieved = nbytes / (ms / 1e3) / 1e9
         kernels["decode_step"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
                                   "GBps": round(achieved, 1)}
@@ -377,7 +395,10 @@ def main():
     else:
         dom = kernels["gate_up"]
         achieved = dom["bytes"] / (dom["us"] / 1e6) / 1e9
-        roofline = {"kernel": "gemv_kernel<1,6,2,SwiGLU> (gate/up 16384x3072 + RMSNorm + SwiGLU)",
+        name = ("gemv_kernel<1,6,2,SwiGLU> (gate/up 16384x3072" if not bits else
+                f"qgemv_kernel<1,{bits},{64 if bits == 8 else 32},3,2> (gate/up 16384x3072, "
+                f"{bits}-bit codes")
+        roofline = {"kernel": f"{name} + RMSNorm + SwiGLU)",
                     "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9,
                     "unit": "GB/s", "frac": round(achieved / (PEAK_HBM / 1e9), 4),
                     "traffic": traffic_from_profiles("gate_up")}
@@ -389,7 +410,7 @@ def main():
         if "OMP_NUM_THREADS" in os.environ:
             threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
         cpu_ref.lib().oracle_set_threads(threads)
-        model = cpu_ref.Model(c, weights)
+        model = cpu_ref.Model(c, weights, bits=bits)
         L0 = args.kv - 1
         cache = model.cache(L0 + 64)
         for layer in range(c["num_hidden_layers"]):
@@ -413,7 +434,9 @@ def main():
             f"({threads} threads)")
 
     line = {
-        "metric": "decode tokens/sec @ batch 1, 3B bf16, KV 4096; % of HBM roofline",
+        "metric": ("decode tokens/sec @ batch 1, 3B bf16, KV 4096; % of HBM roofline" if not bits
+                   else f"decode tokens/sec @ batch 1, 3B {args.precision} (affine group 64), "
+                        f"KV 4096; % of HBM roofline"),
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -423,8 +446,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: random-init N(0,0.02) bf16 weights, unit norm gains, random prompt ids",
+        "dtype": "bf16" if not bits else f"u{bits} codes x bf16 (fp32 accumulate)",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights, unit norm gains, random prompt ids"
+                + ("" if not bits else f"; linears quantized to {bits} bits (affine, group 64)"),
         "config": {"workload": "3B bf16 AR decoder (H3072/F8192/28L/24:8 heads/V83968), "
                                "greedy decode at batch 1 centred on KV length 4096",
                    "batch": 1, "kv_len": args.kv, "prefill_tokens": prefill,

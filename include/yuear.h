@@ -50,25 +50,35 @@ typedef struct yuear_sampling {
   int32_t penalty_window, min_tokens, max_tokens;
 } yuear_sampling;
 
-/* One named bf16 host tensor, names as in the reference checkpoint
+/* One named host tensor, names as in the reference checkpoint
  * (ar.cpp:216-233): model.embed_tokens.weight, model.norm.weight,
  * lm_head.weight, model.layers.{i}.{input_layernorm,post_attention_layernorm,
- * self_attn.{q,k,v,o}_proj,self_attn.{q,k}_norm,mlp.{gate,up,down}_proj}.weight */
+ * self_attn.{q,k,v,o}_proj,self_attn.{q,k}_norm,mlp.{gate,up,down}_proj}.weight.
+ * With affine-quantized linears (ar.cpp:209-214) every *_proj and the
+ * lm_head come as <name>.weight (YUEAR_DTYPE_U32 codes [rows][k * bits / 32])
+ * plus <name>.scales and <name>.biases (bf16 [rows][k / 64]). numel counts
+ * elements of `dtype`. */
+enum { YUEAR_DTYPE_BF16 = 0, YUEAR_DTYPE_U32 = 1 };
 typedef struct yuear_tensor {
   const char *name;
-  const uint16_t *data;
+  const void *data;
   int64_t numel;
+  int32_t dtype;
 } yuear_tensor;
 
 enum { YUEAR_WEIGHTS_RANDOM = 0, YUEAR_WEIGHTS_HOST = 1 };
 typedef struct yuear_weight_source {
   int32_t kind;
-  /* RANDOM: linear/embedding weights N(0, std); norm gains 1 + N(0, norm_std) */
+  /* RANDOM: linear/embedding weights N(0, std); norm gains 1 + N(0, norm_std);
+   * with bits 8 / 4 the linears are then quantized by yuear_quantize_affine */
   uint64_t seed;
   float std, norm_std;
   /* HOST: every tensor of the model exactly once */
   const yuear_tensor *tensors;
   int32_t count;
+  /* 0: bf16 linears; 8 or 4: affine group-64 quantized linears (the
+   * "8bit" / "4bit" precisions, conversion.cpp:470-532) */
+  int32_t bits;
 } yuear_weight_source;
 
 typedef struct yuear_engine yuear_engine;
@@ -93,9 +103,10 @@ void yuear_engine_destroy(yuear_engine *engine);
  * (ar.cpp:161-192 checks; strict != 0 also requires the YuE2 dimensions of
  * ar.cpp:164-178, otherwise any architecture this build implements), then
  * the safetensors file: every tensor of ar.cpp:216-233 with its shape and
- * BF16 dtype and nothing else, with the reference's error messages.
- * precision "8bit"/"4bit" manifests are validated, then refused (bf16
- * weights only). Errors: FileNotFoundError (status 1) for missing files or
+ * dtype and nothing else, with the reference's error messages: BF16, or
+ * for precision "8bit"/"4bit" (manifest bits, group_size 64, mode affine,
+ * linear_only) U32 codes plus BF16 scales and biases for every linear.
+ * Errors: FileNotFoundError (status 1) for missing files or
  * precisions, ValueError (status 2) otherwise. inspect reads and checks the
  * directory without touching the GPU and returns the architecture. */
 yuear_status yuear_checkpoint_inspect(const char *directory, const char *precision,
@@ -103,6 +114,15 @@ yuear_status yuear_checkpoint_inspect(const char *directory, const char *precisi
                                       char **error_json);
 yuear_status yuear_engine_load(const char *directory, const char *precision, int32_t strict,
                                yuear_engine **out, char **error_json);
+/* 0 for bf16 linears, else the quantization bits of the engine's linears. */
+int32_t yuear_engine_bits(const yuear_engine *engine);
+/* Host: affine group-64 quantization of bf16 rows w [rows][k] (k a multiple
+ * of 64) into codes [rows][k * bits / 32] and bf16 scales / biases
+ * [rows][k / 64], as mx::quantize(w, 64, bits, "affine") at
+ * conversion.cpp:508 (restated from MLX's published algorithm: the edge of
+ * larger magnitude is kept exactly as the bias). */
+void yuear_quantize_affine(const uint16_t *w, int64_t rows, int32_t k, int32_t bits,
+                           uint32_t *codes, uint16_t *scales, uint16_t *biases);
 /* Thread-safe cooperative cancellation of the running call (lyra.h:40). */
 void yuear_engine_cancel(yuear_engine *engine);
 /* Deterministic weight generator (host): the bytes RANDOM sources upload. */
@@ -175,7 +195,8 @@ yuear_status yuear_session_set_position(yuear_session *session, int32_t branch,
  * 8 kv heads, 1 or 2 branches); YUEAR_DECODE_FUSED runs QKV + attention +
  * o_proj of a layer as one launch (1 or 2 branches, query heads per kv head
  * 2-4, hidden 256/2048/3072 equal to heads x 128), then gate/up and down.
- * All produce the same bits. They replace the per-op graph of GraphAR
+ * All produce the same bits. Engines with quantized linears use
+ * YUEAR_DECODE_KERNELS only. They replace the per-op graph of GraphAR
  * (cuda_graph.py:43-240). The default is YUEAR_DECODE_KERNELS (the fastest
  * measured on MI355X); YUEAR_DECODE=persistent|fused in the environment
  * when the session begins selects another where available. */
@@ -246,6 +267,17 @@ int32_t yuear_op_attention_decode(
     const uint16_t *dev_rope_sin, uint16_t *dev_k_cache, uint16_t *dev_v_cache,
     const int32_t *dev_pos, int32_t heads, int32_t kv_heads, int32_t capacity,
     int32_t batch, int32_t max_splits, uint16_t *dev_out, void *stream);
+/* Affine group-64 quantized form of yuear_op_gemv for batch 1-2
+ * (mx::quantized_matmul, ar.cpp:22-24): codes [n][k * bits / 32] uint32,
+ * groups [n][k / 64] uint32 words scale | bias << 16 (bf16 halves). */
+int32_t yuear_op_qgemv(const uint32_t *dev_codes, const uint32_t *dev_groups, int32_t bits,
+                       int32_t n, int32_t k, int32_t batch, const uint16_t *dev_x,
+                       int32_t x_stride, const uint16_t *dev_norm_w, float eps,
+                       uint16_t *dev_y, int32_t y_stride, int32_t epilogue, void *stream);
+/* out [n][k] = bf16(s q + b) of quantized rows (layout of yuear_op_qgemv). */
+int32_t yuear_op_dequantize(const uint32_t *dev_codes, const uint32_t *dev_groups,
+                            int32_t bits, int32_t n, int32_t k, uint16_t *dev_out,
+                            void *stream);
 /* C[m][n] = bf16(A[m] . W[n]) (+ C when residual) on MFMA. */
 int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,

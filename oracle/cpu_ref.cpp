@@ -108,6 +108,7 @@ bool phase_of(int phase, int vocab, Phase &p) {
 struct oracle_model {
   oracle_config c;
   oracle_weights w;
+  oracle_quant q;  // q.bits == 0: bf16 linears
 };
 
 struct oracle_cache {
@@ -275,6 +276,66 @@ void oracle_linear(const uint16_t *x, int rows, int k, const uint16_t *w,
   }
 }
 
+// Code j of a packed row (MLX quantize layout: 32 / bits codes per uint32,
+// code j of a word at bits [bits * j, bits * j + bits)).
+static inline uint32_t qcode(const uint32_t *row, int j, int bits) {
+  const int per = 32 / bits;
+  return (row[j / per] >> ((j % per) * bits)) & ((1u << bits) - 1u);
+}
+
+// ar.cpp:22-24: mx::quantized_matmul(x, w, scales, biases, transpose=true,
+// group_size=64, bits, "affine"). Per group g of 64 inputs, fp32 sums of
+// x_i q_i and of x_i; y = bf16(sum_g (s_g * dq_g + b_g * sx_g)).
+void oracle_qlinear(const uint16_t *x, int rows, int k, const uint32_t *w,
+                    const uint16_t *scales, const uint16_t *biases, int bits,
+                    int n, uint16_t *y) {
+  std::vector<float> xf(size_t(rows) * k);
+  for (size_t i = 0; i < xf.size(); ++i)
+    xf[i] = bf2f(x[i]);
+  const int groups = k / 64, words = k * bits / 32;
+#pragma omp parallel for schedule(static)
+  for (int o = 0; o < n; ++o) {
+    const uint32_t *wr = w + size_t(o) * words;
+    const uint16_t *sr = scales + size_t(o) * groups, *br = biases + size_t(o) * groups;
+    for (int r = 0; r < rows; ++r) {
+      const float *xr = xf.data() + size_t(r) * k;
+      if (g_accumulate == 1) {
+        double acc = 0.0;
+        for (int i = 0; i < k; ++i)
+          acc += double(xr[i]) * (double(bf2f(sr[i / 64])) * double(qcode(wr, i, bits)) +
+                                  double(bf2f(br[i / 64])));
+        y[size_t(r) * n + o] = f2bf(float(acc));
+        continue;
+      }
+      float acc = 0.f;
+      for (int g = 0; g < groups; ++g) {
+        float dq[4] = {0.f, 0.f, 0.f, 0.f}, sx[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 64; ++i) {
+          const float xv = xr[g * 64 + i];
+          dq[i & 3] += xv * float(qcode(wr, g * 64 + i, bits));
+          sx[i & 3] += xv;
+        }
+        const float d = (dq[0] + dq[1]) + (dq[2] + dq[3]);
+        const float sum = (sx[0] + sx[1]) + (sx[2] + sx[3]);
+        acc += bf2f(sr[g]) * d + bf2f(br[g]) * sum;
+      }
+      y[size_t(r) * n + o] = f2bf(acc);
+    }
+  }
+}
+
+void oracle_dequantize(const uint32_t *w, const uint16_t *scales,
+                       const uint16_t *biases, int bits, int n, int k,
+                       uint16_t *out) {
+  const int groups = k / 64, words = k * bits / 32;
+  for (int o = 0; o < n; ++o)
+    for (int i = 0; i < k; ++i) {
+      const float s = bf2f(scales[size_t(o) * groups + i / 64]);
+      const float b = bf2f(biases[size_t(o) * groups + i / 64]);
+      out[size_t(o) * k + i] = f2bf(s * float(qcode(w + size_t(o) * words, i, bits)) + b);
+    }
+}
+
 // RoPE tables, ar.cpp:62-74: inv_j = 1 / pow(f32 theta, f32(2j)/f32(D)) in
 // fp32; angle = f32(position) * inv_j; cos/sin rounded to bf16.
 void oracle_rope_table(int positions, int d, double theta, uint16_t *cos_out,
@@ -371,7 +432,17 @@ void oracle_attention(const uint16_t *q, const uint16_t *keys,
 oracle_model *oracle_model_new(const oracle_config *c, const oracle_weights *w) {
   if (!c || !w || c->heads % c->kv_heads || c->head_dim % 2)
     return nullptr;
-  return new oracle_model{*c, *w};
+  return new oracle_model{*c, *w, oracle_quant{}};
+}
+oracle_model *oracle_model_new_quantized(const oracle_config *c, const oracle_weights *w,
+                                         const oracle_quant *q) {
+  if (!q || (q->bits != 8 && q->bits != 4) || c->hidden % 64 || c->intermediate % 64 ||
+      (c->heads * c->head_dim) % 64)
+    return nullptr;
+  oracle_model *m = oracle_model_new(c, w);
+  if (m)
+    m->q = *q;
+  return m;
 }
 void oracle_model_free(oracle_model *m) { delete m; }
 
@@ -398,6 +469,19 @@ uint16_t *oracle_cache_values(oracle_cache *c, int layer) {
   return c->values.data() + c->per_layer * layer;
 }
 
+// Projection `kind` (0..6 = q, k, v, o, gate, up, down) of one layer.
+static void layer_linear(const oracle_model *m, int layer, int kind, const uint16_t *x, int T,
+                         int k, int n, uint16_t *y) {
+  const oracle_weights &w = m->w;
+  const uint16_t *const *tables[7] = {w.wq, w.wk, w.wv, w.wo, w.wg, w.wu, w.wd};
+  const uint16_t *wt = tables[kind][layer];
+  if (m->q.bits)
+    oracle_qlinear(x, T, k, reinterpret_cast<const uint32_t *>(wt), m->q.scales[kind][layer],
+                   m->q.biases[kind][layer], m->q.bits, n, y);
+  else
+    oracle_linear(x, T, k, wt, n, y);
+}
+
 // One decoder layer, ar.cpp:265-298.
 int oracle_layer(oracle_model *m, oracle_cache *cache, int layer, uint16_t *x,
                  int T) {
@@ -413,9 +497,9 @@ int oracle_layer(oracle_model *m, oracle_cache *cache, int layer, uint16_t *x,
       o(size_t(T) * H), g(size_t(T) * F), u(size_t(T) * F), mm(size_t(T) * F),
       dn(size_t(T) * H), qn(q.size()), kn(k.size());
   oracle_rms_norm(x, T, H, w.input_ln[layer], c.rms_eps, h.data());
-  oracle_linear(h.data(), T, H, w.wq[layer], Hq * D, q.data());
-  oracle_linear(h.data(), T, H, w.wk[layer], Hkv * D, k.data());
-  oracle_linear(h.data(), T, H, w.wv[layer], Hkv * D, v.data());
+  layer_linear(m, layer, 0, h.data(), T, H, Hq * D, q.data());
+  layer_linear(m, layer, 1, h.data(), T, H, Hkv * D, k.data());
+  layer_linear(m, layer, 2, h.data(), T, H, Hkv * D, v.data());
   if (c.qk_norm) {  // ar.cpp:268-275: RMSNorm over D per head
     oracle_rms_norm(q.data(), T * Hq, D, w.q_norm[layer], c.rms_eps, qn.data());
     oracle_rms_norm(k.data(), T * Hkv, D, w.k_norm[layer], c.rms_eps, kn.data());
@@ -435,14 +519,14 @@ int oracle_layer(oracle_model *m, oracle_cache *cache, int layer, uint16_t *x,
       }
   oracle_attention(q.data(), K, V, T, Hq, Hkv, D, cache->capacity, offset,
                    att.data());
-  oracle_linear(att.data(), T, Hq * D, w.wo[layer], H, o.data());
+  layer_linear(m, layer, 3, att.data(), T, Hq * D, H, o.data());
   for (size_t i = 0; i < size_t(T) * H; ++i)  // ar.cpp:292-294
     x[i] = f2bf(bf2f(x[i]) + bf2f(o[i]));
   oracle_rms_norm(x, T, H, w.post_ln[layer], c.rms_eps, h.data());
-  oracle_linear(h.data(), T, H, w.wg[layer], F, g.data());
-  oracle_linear(h.data(), T, H, w.wu[layer], F, u.data());
+  layer_linear(m, layer, 4, h.data(), T, H, F, g.data());
+  layer_linear(m, layer, 5, h.data(), T, H, F, u.data());
   oracle_silu_mul(g.data(), u.data(), T * F, mm.data());
-  oracle_linear(mm.data(), T, F, w.wd[layer], H, dn.data());
+  layer_linear(m, layer, 6, mm.data(), T, F, H, dn.data());
   for (size_t i = 0; i < size_t(T) * H; ++i)  // ar.cpp:295-298
     x[i] = f2bf(bf2f(x[i]) + bf2f(dn[i]));
   return 0;
@@ -481,6 +565,18 @@ int oracle_project(oracle_model *m, const uint16_t *h, int phase,
   if (!phase_of(phase, m->c.vocab, p))
     return 2;
   const int H = m->c.hidden;
+  if (m->q.bits) {  // ar.cpp:306-312: quantized rows, one row range at a time
+    const uint32_t *qw = reinterpret_cast<const uint32_t *>(m->w.lm_head);
+    const size_t words = size_t(H) * m->q.bits / 32, groups = H / 64;
+    auto range = [&](int start, int len, uint16_t *out) {
+      oracle_qlinear(h, 1, H, qw + start * words, m->q.lm_scales + start * groups,
+                     m->q.lm_biases + start * groups, m->q.bits, len, out);
+    };
+    range(p.seg0_start, p.seg0_len, logits);
+    if (p.size > p.seg0_len)
+      range(p.seg1_start, p.size - p.seg0_len, logits + p.seg0_len);
+    return 0;
+  }
   std::vector<float> hf(H);
   for (int i = 0; i < H; ++i)
     hf[i] = bf2f(h[i]);

@@ -20,6 +20,14 @@
  *   bf16 RNE, Philox4x32-10 ....... published Random123 KAT + rocRAND fixture
  *   rms_norm ...................... closed form; constant-row special case
  *   linear ........................ fp64 brute force; one-hot weights
+ *   qlinear / dequantize .......... fp64 brute force over the unpacked codes;
+ *                                   equality with linear when every s q + b is
+ *                                   a bf16 value; zero codes give the bias
+ *                                   term alone. The U32 packing order (MLX
+ *                                   quantize: element j of a word at bits
+ *                                   bits * j) is parity unpinned: MLX is
+ *                                   absent and the reference holds no
+ *                                   quantized fixture.
  *   rope .......................... position 0 identity; norm preservation
  *   silu_mul ...................... reference test_ar.py known answers
  *   attention ..................... fp64 brute force; split-merge identity;
@@ -55,6 +63,18 @@ typedef struct oracle_weights {
   const uint16_t *const *wg, *const *wu, *const *wd;
 } oracle_weights;
 
+/* Affine group-64 quantized linears (ar.cpp:20-29, 209-214; the
+ * conversion.cpp:470-532 layout): when bits is 8 or 4, the seven projection
+ * pointers of oracle_weights and lm_head point to packed uint32 codes
+ * [rows][k * bits / 32] and scales / biases hold [rows][k / 64] bf16 per
+ * linear (index 0..6 = q, k, v, o, gate, up, down; [layers] each). */
+typedef struct oracle_quant {
+  int32_t bits;
+  const uint16_t *lm_scales, *lm_biases;
+  const uint16_t *const *scales[7];
+  const uint16_t *const *biases[7];
+} oracle_quant;
+
 typedef struct oracle_sampling {
   double temperature, top_p;
   int32_t top_k;
@@ -84,6 +104,16 @@ void oracle_rms_norm(const uint16_t *x, int rows, int n, const uint16_t *w,
                      float eps, uint16_t *y);
 void oracle_linear(const uint16_t *x, int rows, int k, const uint16_t *w,
                    int n, uint16_t *y);
+/* mx::quantized_matmul(x, w, scales, biases, transpose=true, 64, bits,
+ * "affine") (ar.cpp:22-24): y = bf16(sum_g (s_g * sum_{i in g} x_i q_i +
+ * b_g * sum_{i in g} x_i)), fp32 sums per group and over groups. */
+void oracle_qlinear(const uint16_t *x, int rows, int k, const uint32_t *w,
+                    const uint16_t *scales, const uint16_t *biases, int bits,
+                    int n, uint16_t *y);
+/* bf16(s * q + b) per element (s * q is exact in fp32; one fp32 add). */
+void oracle_dequantize(const uint32_t *w, const uint16_t *scales,
+                       const uint16_t *biases, int bits, int n, int k,
+                       uint16_t *out);
 void oracle_rope(uint16_t *x, int T, int heads, int d, int offset,
                  double theta);
 void oracle_silu_mul(const uint16_t *g, const uint16_t *u, int n,
@@ -99,6 +129,9 @@ void oracle_rope_table(int positions, int d, double theta, uint16_t *cos_out,
 
 /* ---- model / cache (ar.cpp:98-132, 246-323) ---- */
 oracle_model *oracle_model_new(const oracle_config *c, const oracle_weights *w);
+/* As oracle_model_new with affine-quantized linears (q->bits 8 or 4). */
+oracle_model *oracle_model_new_quantized(const oracle_config *c, const oracle_weights *w,
+                                         const oracle_quant *q);
 void oracle_model_free(oracle_model *m);
 oracle_cache *oracle_cache_new(const oracle_model *m, int capacity);
 void oracle_cache_free(oracle_cache *c);

@@ -19,6 +19,7 @@ PHASES = {"full": 0, "abc": 1, "semantic": 2}
 
 u16p = C.POINTER(C.c_uint16)
 i32p = C.POINTER(C.c_int32)
+u32p = C.POINTER(C.c_uint32)
 f32p = C.POINTER(C.c_float)
 
 
@@ -33,6 +34,15 @@ class Weights(C.Structure):
     _fields_ = [(name, u16p) for name in ("embed", "final_norm", "lm_head")] + [
         (name, C.POINTER(u16p)) for name in
         ("input_ln", "post_ln", "q_norm", "k_norm", "wq", "wk", "wv", "wo", "wg", "wu", "wd")]
+
+
+LINEARS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+           "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+class Quant(C.Structure):
+    _fields_ = [("bits", C.c_int32), ("lm_scales", u16p), ("lm_biases", u16p),
+                ("scales", C.POINTER(u16p) * 7), ("biases", C.POINTER(u16p) * 7)]
 
 
 class Sampling(C.Structure):
@@ -67,6 +77,11 @@ def _load():
         "oracle_attention": (None, [u16p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int,
                                     C.c_int, C.c_int, u16p]),
         "oracle_model_new": (C.c_void_p, [C.POINTER(Config), C.POINTER(Weights)]),
+        "oracle_model_new_quantized": (C.c_void_p, [C.POINTER(Config), C.POINTER(Weights),
+                                                    C.POINTER(Quant)]),
+        "oracle_qlinear": (None, [u16p, C.c_int, C.c_int, u32p, u16p, u16p, C.c_int, C.c_int,
+                                  u16p]),
+        "oracle_dequantize": (None, [u32p, u16p, u16p, C.c_int, C.c_int, C.c_int, u16p]),
         "oracle_model_free": (None, [C.c_void_p]),
         "oracle_cache_new": (C.c_void_p, [C.c_void_p, C.c_int]),
         "oracle_cache_free": (None, [C.c_void_p]),
@@ -140,6 +155,30 @@ def linear(x, w):
     y = np.empty(x.shape[:-1] + (n,), dtype=np.uint16)
     lib().oracle_linear(px, x.size // k, k, pw, n, y.ctypes.data_as(u16p))
     return y
+
+
+def qlinear(x, wq, scales, biases, bits):
+    """Affine group-64 quantized linear: wq [n][k * bits / 32] uint32 codes,
+    scales / biases [n][k / 64] bf16."""
+    x, px = _u16(x)
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    scales, ps = _u16(scales)
+    biases, pb = _u16(biases)
+    n, k = scales.shape[0], scales.shape[1] * 64
+    y = np.empty(x.shape[:-1] + (n,), dtype=np.uint16)
+    lib().oracle_qlinear(px, x.size // k, k, wq.ctypes.data_as(u32p), ps, pb, bits, n,
+                         y.ctypes.data_as(u16p))
+    return y
+
+
+def dequantize(wq, scales, biases, bits):
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    scales, ps = _u16(scales)
+    biases, pb = _u16(biases)
+    n, k = scales.shape[0], scales.shape[1] * 64
+    out = np.empty((n, k), dtype=np.uint16)
+    lib().oracle_dequantize(wq.ctypes.data_as(u32p), ps, pb, bits, n, k, out.ctypes.data_as(u16p))
+    return out
 
 
 def rope(x, offset, theta):
@@ -228,9 +267,13 @@ LAYER_TENSORS = [("input_ln", "input_layernorm"), ("post_ln", "post_attention_la
 class Model:
     """Oracle ARModel over host weights keyed by the reference tensor names."""
 
-    def __init__(self, config: dict, weights: dict):
+    def __init__(self, config: dict, weights: dict, bits: int = 0):
+        """bits 8 / 4: the projections and lm_head are affine group-64 quantized
+        (``<name>.weight`` uint32 codes, ``<name>.scales`` / ``<name>.biases`` bf16)."""
         self.config = dict(config)
-        self.weights = {k: np.ascontiguousarray(v, dtype=np.uint16) for k, v in weights.items()}
+        self.bits = bits
+        self.weights = {k: np.ascontiguousarray(v, dtype=np.uint32 if v.dtype == np.uint32
+                                                else np.uint16) for k, v in weights.items()}
         c = self.config
         self._cfg = Config(c["hidden_size"], c["intermediate_size"], c["num_hidden_layers"],
                            c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"],
@@ -248,7 +291,20 @@ class Model:
         self._w = Weights(w["model.embed_tokens.weight"].ctypes.data_as(u16p),
                           w["model.norm.weight"].ctypes.data_as(u16p),
                           w["lm_head.weight"].ctypes.data_as(u16p), **fields)
-        self.handle = lib().oracle_model_new(C.byref(self._cfg), C.byref(self._w))
+        if bits:
+            def table(suffix):
+                arr = (u16p * L)(*[w[f"model.layers.{i}.{suffix}"].ctypes.data_as(u16p)
+                                   for i in range(L)])
+                self._arrays[suffix] = arr
+                return C.cast(arr, C.POINTER(u16p))
+            self._q = Quant(bits, w["lm_head.scales"].ctypes.data_as(u16p),
+                            w["lm_head.biases"].ctypes.data_as(u16p),
+                            (C.POINTER(u16p) * 7)(*[table(n + ".scales") for n in LINEARS]),
+                            (C.POINTER(u16p) * 7)(*[table(n + ".biases") for n in LINEARS]))
+            self.handle = lib().oracle_model_new_quantized(C.byref(self._cfg), C.byref(self._w),
+                                                           C.byref(self._q))
+        else:
+            self.handle = lib().oracle_model_new(C.byref(self._cfg), C.byref(self._w))
         if not self.handle:
             raise ValueError("invalid oracle model configuration")
 

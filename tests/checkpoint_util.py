@@ -3,7 +3,7 @@
 A directory holds conversion.json (the schema-1 manifest of
 native/src/conversion.cpp:609-693, reduced to what ARModel reads,
 ar.cpp:137-160), config.json and ar-<precision>.safetensors. Tensors are
-bf16 bit patterns (uint16). `write_safetensors` writes the format directly
+bf16 bit patterns (uint16) or, for the quantized precisions' codes, uint32. `write_safetensors` writes the format directly
 (8-byte little-endian header length, JSON header, data) so that malformed
 files can be made; `write_checkpoint(..., writer="safetensors")` uses the
 safetensors package instead, to check files made by the official writer.
@@ -35,16 +35,24 @@ def hf_config(cfg):
     return out
 
 
+def _raw(arr):
+    """(dtype name, little-endian bytes) of a bf16 (uint16) or U32 (uint32) array."""
+    if np.asarray(arr).dtype == np.uint32:
+        return "U32", np.ascontiguousarray(arr, dtype="<u4").tobytes()
+    return "BF16", np.ascontiguousarray(arr, dtype="<u2").tobytes()
+
+
 def write_safetensors(path, tensors, dtypes=None, shapes=None, offsets=None, pad_odd=False):
-    """tensors: name -> uint16 array. dtypes/shapes/offsets override header fields;
-    pad_odd puts one byte before the data so that tensors sit at odd offsets."""
+    """tensors: name -> uint16 (BF16) or uint32 (U32) array. dtypes/shapes/offsets
+    override header fields; pad_odd puts one byte before the data so that
+    tensors sit at odd offsets."""
     dtypes, shapes, offsets = dtypes or {}, shapes or {}, offsets or {}
     header, blobs, pos = {}, [], 1 if pad_odd else 0
     if pad_odd:
         blobs.append(b"\0")
     for name in sorted(tensors):
-        raw = np.ascontiguousarray(tensors[name], dtype=np.uint16).tobytes()
-        header[name] = {"dtype": dtypes.get(name, "BF16"),
+        kind, raw = _raw(tensors[name])
+        header[name] = {"dtype": dtypes.get(name, kind),
                         "shape": list(shapes.get(name, np.shape(tensors[name]))),
                         "data_offsets": list(offsets.get(name, (pos, pos + len(raw))))}
         blobs.append(raw)
@@ -77,8 +85,13 @@ def write_checkpoint(directory, cfg, weights, precision="bf16", writer="raw", ma
         import torch
         from safetensors.torch import save_file
 
-        save_file({k: torch.from_numpy(np.ascontiguousarray(v, dtype=np.uint16).view(np.int16))
-                   .view(torch.bfloat16) for k, v in weights.items()}, path)
+        def tensor(v):
+            if np.asarray(v).dtype == np.uint32:
+                return torch.from_numpy(np.ascontiguousarray(v).view(np.int32)).view(torch.uint32)
+            return torch.from_numpy(np.ascontiguousarray(v, dtype=np.uint16).view(np.int16)).view(
+                torch.bfloat16)
+
+        save_file({k: tensor(v) for k, v in weights.items()}, path)
     else:
         write_safetensors(path, weights, **st_kwargs)
     return directory

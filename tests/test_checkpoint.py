@@ -1,5 +1,6 @@
 """Checkpoint directory loader (ARModel(directory, precision), ar.cpp:133-238)
-on the CPU: yuear_checkpoint_inspect reads and validates conversion.json,
+on the CPU, for the bf16 and the affine-quantized ("8bit" / "4bit")
+precisions: yuear_checkpoint_inspect reads and validates conversion.json,
 config.json and the safetensors header without touching the GPU. Every
 message checked here is the reference's own (ar.cpp:137-236)."""
 import json
@@ -10,6 +11,7 @@ import pytest
 
 from checkpoint_util import write_checkpoint, write_safetensors
 from conftest import TINY
+from quant_util import quantize_model
 
 
 @pytest.fixture(scope="module")
@@ -101,10 +103,43 @@ def test_manifest_checks(yuear_lib, weights, tmp_path, patch, kind, message):
         inspect(yuear_lib, d)
 
 
-def test_quantized_precisions_are_validated_then_refused(yuear_lib, weights, tmp_path):
-    d = write_checkpoint(tmp_path / "q", TINY, weights, precision="4bit")
-    with pytest.raises(ValueError, match="not supported by this build"):
-        inspect(yuear_lib, d, "4bit")
+@pytest.mark.parametrize("writer", ["raw", "safetensors"])
+@pytest.mark.parametrize("precision,bits", [("8bit", 8), ("4bit", 4)])
+def test_quantized_precisions_are_accepted(yuear_lib, weights, tmp_path, writer, precision, bits):
+    q = quantize_model(weights, bits)
+    d = write_checkpoint(tmp_path / "q", TINY, q, precision=precision, writer=writer)
+    assert inspect(yuear_lib, d, precision)["hidden_size"] == TINY["hidden_size"]
+    # the bf16 file of the same directory is not what the manifest names
+    with pytest.raises(FileNotFoundError, match="does not contain bf16 AR weights"):
+        inspect(yuear_lib, d, "bf16")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantized_tensor_checks(yuear_lib, weights, tmp_path, bits):
+    precision = f"{bits}bit"
+    q = quantize_model(weights, bits)
+    name = "model.layers.0.mlp.down_proj"
+    H, F = TINY["hidden_size"], TINY["intermediate_size"]
+    cases = [
+        # bf16 codes where U32 is required (an unquantized linear in a quantized file)
+        (dict(q, **{name + ".weight": weights[name + ".weight"]}),
+         {}, f"Incompatible AR tensor shape/dtype: {name}.weight"),
+        (q, {"shapes": {name + ".weight": (H, F * bits // 32 + 1)}},
+         f"Incompatible AR tensor shape/dtype: {name}.weight"),
+        (q, {"dtypes": {name + ".scales": "F16"}}, f"Incompatible AR tensor shape/dtype: {name}.scales"),
+        ({k: v for k, v in q.items() if k != name + ".biases"}, {}, f"Missing AR tensor: {name}.biases"),
+        (dict(q, **{"model.norm.scales": np.zeros(4, np.uint16)}), {},
+         "Unexpected AR tensor: model.norm.scales"),
+        (q, {"offsets": {name + ".weight": (0, 4)}}, f"invalid data offsets for {name}.weight"),
+    ]
+    for i, (tensors, kw, message) in enumerate(cases):
+        d = write_checkpoint(tmp_path / str(i), TINY, {}, precision=precision)
+        write_safetensors(d / f"ar-{precision}.safetensors", tensors, **kw)
+        with pytest.raises(ValueError, match=message):
+            inspect(yuear_lib, d, precision)
+
+
+def test_quantized_settings_and_precision_names(yuear_lib, weights, tmp_path):
     d = write_checkpoint(tmp_path / "g", TINY, weights, precision="8bit",
                          manifest_patch=lambda m: m["precisions"]["8bit"].update(group_size=32))
     with pytest.raises(ValueError, match="Invalid affine quantization settings"):

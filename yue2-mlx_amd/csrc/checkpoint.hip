@@ -12,8 +12,10 @@
 // Every tensor the reference requires must be present with its shape and
 // dtype and nothing else (ar.cpp:193-236, same messages). The file is mapped
 // read-only and its tensors are handed to yuear_engine_create, which copies
-// them to the device. Affine-quantized precisions are validated like the
-// reference and then refused: this build streams bf16 weights only.
+// them to the device. With the affine-quantized precisions every linear (the
+// seven projections of each layer and the lm_head) is U32 codes
+// [rows][k * bits / 32] plus BF16 scales and biases [rows][k / 64]
+// (ar.cpp:209-214); the embedding and the norms stay BF16.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -173,31 +175,48 @@ struct Loaded {
   Mapping map;
   std::vector<std::string> names;
   std::vector<yuear_tensor> tensors;
-  std::vector<std::vector<uint16_t>> realigned;  // tensors at odd byte offsets
+  // tensors whose file offset is not a multiple of their element size
+  std::vector<std::vector<uint32_t>> realigned;
 };
 
-// The expected tensors and shapes (ar.cpp:193-233) for a config.
-std::map<std::string, std::vector<long long>> expected_tensors(const yuear_model_config &k) {
+struct TensorSpec {
+  std::vector<long long> shape;
+  bool u32;  // U32 codes, else BF16
+};
+
+// The expected tensors, shapes and dtypes (ar.cpp:193-233) for a config and
+// the quantization bits (0: bf16).
+std::map<std::string, TensorSpec> expected_tensors(const yuear_model_config &k, int bits) {
   const long long H = k.hidden_size, F = k.intermediate_size, D = k.head_dim,
                   Q = k.num_attention_heads * D, KV = k.num_key_value_heads * D,
                   V = k.vocab_size;
-  std::map<std::string, std::vector<long long>> e;
-  e["model.embed_tokens.weight"] = {V, H};
-  e["model.norm.weight"] = {H};
-  e["lm_head.weight"] = {V, H};
+  std::map<std::string, TensorSpec> e;
+  auto norm = [&](const std::string &n, long long width) { e[n + ".weight"] = {{width}, false}; };
+  auto linear = [&](const std::string &n, long long out, long long in) {
+    if (!bits) {
+      e[n + ".weight"] = {{out, in}, false};
+      return;
+    }
+    e[n + ".weight"] = {{out, in * bits / 32}, true};
+    e[n + ".scales"] = {{out, in / 64}, false};
+    e[n + ".biases"] = {{out, in / 64}, false};
+  };
+  e["model.embed_tokens.weight"] = {{V, H}, false};
+  norm("model.norm", H);
+  linear("lm_head", V, H);
   for (int i = 0; i < k.num_hidden_layers; ++i) {
     const std::string n = "model.layers." + std::to_string(i);
-    e[n + ".input_layernorm.weight"] = {H};
-    e[n + ".post_attention_layernorm.weight"] = {H};
-    e[n + ".self_attn.q_norm.weight"] = {D};
-    e[n + ".self_attn.k_norm.weight"] = {D};
-    e[n + ".self_attn.q_proj.weight"] = {Q, H};
-    e[n + ".self_attn.k_proj.weight"] = {KV, H};
-    e[n + ".self_attn.v_proj.weight"] = {KV, H};
-    e[n + ".self_attn.o_proj.weight"] = {H, Q};
-    e[n + ".mlp.gate_proj.weight"] = {F, H};
-    e[n + ".mlp.up_proj.weight"] = {F, H};
-    e[n + ".mlp.down_proj.weight"] = {H, F};
+    norm(n + ".input_layernorm", H);
+    norm(n + ".post_attention_layernorm", H);
+    norm(n + ".self_attn.q_norm", D);
+    norm(n + ".self_attn.k_norm", D);
+    linear(n + ".self_attn.q_proj", Q, H);
+    linear(n + ".self_attn.k_proj", KV, H);
+    linear(n + ".self_attn.v_proj", KV, H);
+    linear(n + ".self_attn.o_proj", H, Q);
+    linear(n + ".mlp.gate_proj", F, H);
+    linear(n + ".mlp.up_proj", F, H);
+    linear(n + ".mlp.down_proj", H, F);
   }
   return e;
 }
@@ -211,9 +230,7 @@ void open_checkpoint(const std::string &dir, const std::string &precision, bool 
     throw Error("FileNotFoundError", dir);
   const std::string filename = check_manifest(read_json(dir + "/conversion.json"), precision);
   out.config = check_config(read_json(dir + "/config.json"), strict);
-  if (precision != "bf16")
-    invalid("precision '" + precision +
-            "' AR weights are not supported by this build (bf16 weights only)");
+  const int bits = precision == "bf16" ? 0 : precision == "8bit" ? 8 : 4;
 
   const std::string path = dir + "/" + filename;
   const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
@@ -259,7 +276,7 @@ void open_checkpoint(const std::string &dir, const std::string &precision, bool 
     invalid(filename + ": safetensors header must be a JSON object");
   const size_t data0 = 8 + size_t(hlen), data_bytes = file_bytes - data0;
 
-  const auto expected = expected_tensors(out.config);
+  const auto expected = expected_tensors(out.config, bits);
   std::set<std::string> seen;
   for (const auto &[name, t] : h.obj) {
     if (name == "__metadata__")
@@ -268,12 +285,14 @@ void open_checkpoint(const std::string &dir, const std::string &precision, bool 
     if (it == expected.end())
       invalid("Unexpected AR tensor: " + name);
     const json::Value *dt = t.get("dtype"), *shape = t.get("shape"), *offs = t.get("data_offsets");
-    bool ok = dt && dt->is_string() && dt->str == "BF16" && shape && shape->is_array() &&
-              shape->arr.size() == it->second.size();
+    const TensorSpec &spec = it->second;
+    const long long esize = spec.u32 ? 4 : 2;
+    bool ok = dt && dt->is_string() && dt->str == (spec.u32 ? "U32" : "BF16") && shape &&
+              shape->is_array() && shape->arr.size() == spec.shape.size();
     long long numel = 1;
     for (size_t d = 0; ok && d < shape->arr.size(); ++d) {
       const json::Value &s = shape->arr[d];
-      ok = is_int(&s) && s.inum == it->second[d];
+      ok = is_int(&s) && s.inum == spec.shape[d];
       numel *= ok ? s.inum : 1;
     }
     if (!ok)
@@ -281,22 +300,22 @@ void open_checkpoint(const std::string &dir, const std::string &precision, bool 
     if (!offs || !offs->is_array() || offs->arr.size() != 2 || !is_int(&offs->arr[0]) ||
         !is_int(&offs->arr[1]) || offs->arr[0].inum < 0 || offs->arr[1].inum < offs->arr[0].inum ||
         uint64_t(offs->arr[1].inum) > data_bytes ||
-        offs->arr[1].inum - offs->arr[0].inum != numel * 2)
+        offs->arr[1].inum - offs->arr[0].inum != numel * esize)
       invalid(filename + ": invalid data offsets for " + name);
     seen.insert(name);
     if (map_data) {
       const size_t at = data0 + size_t(offs->arr[0].inum);
       const unsigned char *p = static_cast<const unsigned char *>(out.map.base) + at;
-      const uint16_t *data;
-      if (at % 2) {  // safetensors does not promise alignment
-        out.realigned.emplace_back(size_t(numel));
-        std::memcpy(out.realigned.back().data(), p, size_t(numel) * 2);
+      const void *data = p;
+      if (at % size_t(esize)) {  // safetensors does not promise alignment
+        const size_t bytes = size_t(numel * esize);
+        out.realigned.emplace_back((bytes + 3) / 4);
+        std::memcpy(out.realigned.back().data(), p, bytes);
         data = out.realigned.back().data();
-      } else {
-        data = reinterpret_cast<const uint16_t *>(p);
       }
       out.names.push_back(name);
-      out.tensors.push_back(yuear_tensor{nullptr, data, numel});
+      out.tensors.push_back(yuear_tensor{nullptr, data, numel,
+                                         spec.u32 ? YUEAR_DTYPE_U32 : YUEAR_DTYPE_BF16});
     }
   }
   for (const auto &kv : expected)
@@ -344,5 +363,7 @@ extern "C" yuear_status yuear_engine_load(const char *directory, const char *pre
   src.kind = YUEAR_WEIGHTS_HOST;
   src.tensors = ck->tensors.data();
   src.count = int32_t(ck->tensors.size());
+  const std::string prec = precision ? precision : "bf16";
+  src.bits = prec == "8bit" ? 8 : prec == "4bit" ? 4 : 0;
   return yuear_engine_create(&ck->config, &src, out, error_json);
 }

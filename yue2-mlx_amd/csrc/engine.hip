@@ -165,6 +165,10 @@ size_t align_elems(size_t n) { return (n + 127) & ~size_t(127); }  // 256 B
 
 struct LayerW {
   uint16_t *input_ln, *post_ln, *q_norm, *k_norm, *qkv, *o, *gu, *down;
+  // quantized linears: codes and group words (scale | bias << 16) of the
+  // same rows; qkv / o / gu / down then hold their dequantized rows
+  const uint32_t *qqkv = nullptr, *gqkv = nullptr, *qo = nullptr, *go = nullptr;
+  const uint32_t *qgu = nullptr, *ggu = nullptr, *qdown = nullptr, *gdown = nullptr;
   // MFMA-tiled copies of the projections for batched decode (launch_tile_rows)
   uint16_t *qkv_t = nullptr, *o_t = nullptr, *gu_t = nullptr, *down_t = nullptr;
 };
@@ -228,6 +232,9 @@ struct yuear_engine {
   uint16_t *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
   std::vector<LayerW> layers;
   uint16_t *rope_cos = nullptr, *rope_sin = nullptr;
+  int bits = 0;                  // 0: bf16 linears; 8 / 4: affine group-64 quantized
+  uint32_t *qweights = nullptr;  // codes and group words of every quantized linear
+  const uint32_t *lm_q = nullptr, *lm_g = nullptr;
   // MFMA-tiled projection copies, built by the first session of 3+ branches
   // (6.15 GB more at the 3B shape: HBM is plentiful, the batched GEMVs read
   // 1 KiB contiguous per wave-load from them)
@@ -238,6 +245,7 @@ struct yuear_engine {
 
   ~yuear_engine() {
     if (weights) (void)hipFree(weights);
+    if (qweights) (void)hipFree(qweights);
     if (rope_cos) (void)hipFree(rope_cos);
     if (tiled) (void)hipFree(tiled);
   }
@@ -333,16 +341,22 @@ namespace {
 void build_engine(yuear_engine &E, const yuear_weight_source *src) {
   const Config &c = E.cfg;
   HIPC(hipGetDevice(&E.device));
-  // device layout
-  struct Item {
-    std::string name;
-    size_t numel;
-    int kind;  // 0 plain, 1 q/k/v part, 2 gate/up part
-  };
+  if (!src)
+    invalid("a weight source is required");
+  const int bits = src->bits;
+  if (bits != 0 && bits != 8 && bits != 4)
+    invalid("weight bits must be 0 (bf16), 8 or 4");
+  if (bits && !(qgemv_supported(bits, c.H, 1) && qgemv_supported(bits, c.Hq * c.D, 1) &&
+                qgemv_supported(bits, c.F, 1)))
+    invalid("quantized linears need input widths that the quantized GEMV implements");
+  E.bits = bits;
   auto layer_name = [](int i, int j) {
     return "model.layers." + std::to_string(i) + "." + kLayerNames[j] + ".weight";
   };
+  auto base_of = [](const std::string &weight) { return weight.substr(0, weight.size() - 7); };
   const size_t Hs = c.H, Fs = c.F, Vs = c.V, QD = size_t(c.Hq) * c.D, KD = size_t(c.Hkv) * c.D;
+  // device layout: bf16 tensors (with quantized linears, their dequantized
+  // rows, read by prefill and the batched GEMVs)
   size_t total = align_elems(Vs * Hs) * 2 + align_elems(Hs);
   const size_t per_layer = align_elems(Hs) * 2 + align_elems(c.D) * 2 +
                            align_elems((QD + 2 * KD) * Hs) + align_elems(Hs * QD) +
@@ -370,21 +384,62 @@ void build_engine(yuear_engine &E, const yuear_weight_source *src) {
     L.gu = take(2 * Fs * Hs);
     L.down = take(Hs * Fs);
   }
+  // quantized linears: codes [rows][k * bits / 32] and group words [rows][k / 64]
+  auto qwords = [&](size_t rows, size_t k) {
+    return align_elems(rows * k * bits / 32) + align_elems(rows * k / 64);
+  };
+  if (bits) {
+    size_t words = qwords(Vs, Hs);
+    words += c.layers * (qwords(QD + 2 * KD, Hs) + qwords(Hs, QD) + qwords(2 * Fs, Hs) +
+                         qwords(Hs, Fs));
+    HIPC(hipMalloc(&E.qweights, words * 4));
+    E.weight_bytes += words * 4;
+    uint32_t *qc = E.qweights;
+    auto qtake = [&](size_t rows, size_t k, const uint32_t *&codes, const uint32_t *&groups) {
+      codes = qc;
+      qc += align_elems(rows * k * bits / 32);
+      groups = qc;
+      qc += align_elems(rows * k / 64);
+    };
+    qtake(Vs, Hs, E.lm_q, E.lm_g);
+    for (auto &L : E.layers) {
+      qtake(QD + 2 * KD, Hs, L.qqkv, L.gqkv);
+      qtake(Hs, QD, L.qo, L.go);
+      qtake(2 * Fs, Hs, L.qgu, L.ggu);
+      qtake(Hs, Fs, L.qdown, L.gdown);
+    }
+  }
 
-  // expected tensors (ar.cpp:216-233)
-  std::map<std::string, size_t> expected;
-  expected["model.embed_tokens.weight"] = Vs * Hs;
-  expected["model.norm.weight"] = Hs;
-  expected["lm_head.weight"] = Vs * Hs;
-  const size_t sizes[kNumLayerTensors] = {Hs, Hs, size_t(c.D), size_t(c.D), QD * Hs, KD * Hs,
-                                          KD * Hs, Hs * QD, Fs * Hs, Fs * Hs, Hs * Fs};
+  // expected tensors (ar.cpp:209-233)
+  struct Spec {
+    size_t numel;
+    int dtype;
+  };
+  std::map<std::string, Spec> expected;
+  auto linear = [&](const std::string &weight, size_t rows, size_t k) {
+    if (!bits) {
+      expected[weight] = {rows * k, YUEAR_DTYPE_BF16};
+      return;
+    }
+    expected[weight] = {rows * k * bits / 32, YUEAR_DTYPE_U32};
+    expected[base_of(weight) + ".scales"] = {rows * k / 64, YUEAR_DTYPE_BF16};
+    expected[base_of(weight) + ".biases"] = {rows * k / 64, YUEAR_DTYPE_BF16};
+  };
+  expected["model.embed_tokens.weight"] = {Vs * Hs, YUEAR_DTYPE_BF16};
+  expected["model.norm.weight"] = {Hs, YUEAR_DTYPE_BF16};
+  linear("lm_head.weight", Vs, Hs);
+  const size_t rows[kNumLayerTensors] = {Hs, Hs, size_t(c.D), size_t(c.D), QD, KD, KD, Hs, Fs, Fs,
+                                         Hs};
+  const size_t cols[kNumLayerTensors] = {1, 1, 1, 1, Hs, Hs, Hs, QD, Hs, Hs, Fs};
   for (int i = 0; i < c.layers; ++i)
-    for (int j = 0; j < kNumLayerTensors; ++j)
-      expected[layer_name(i, j)] = sizes[j];
+    for (int j = 0; j < kNumLayerTensors; ++j) {
+      if (j < 4)
+        expected[layer_name(i, j)] = {rows[j], YUEAR_DTYPE_BF16};
+      else
+        linear(layer_name(i, j), rows[j], cols[j]);
+    }
 
-  std::map<std::string, const uint16_t *> host;
-  if (!src)
-    invalid("a weight source is required");
+  std::map<std::string, const void *> host;
   if (src->kind == YUEAR_WEIGHTS_HOST) {
     if (!src->tensors || src->count < 0)
       invalid("host weight source needs a tensor table");
@@ -395,7 +450,7 @@ void build_engine(yuear_engine &E, const yuear_weight_source *src) {
       auto it = expected.find(tt.name);
       if (it == expected.end())
         invalid(std::string("Unexpected AR tensor: ") + tt.name);
-      if (size_t(tt.numel) != it->second)
+      if (size_t(tt.numel) != it->second.numel || tt.dtype != it->second.dtype)
         invalid(std::string("Incompatible AR tensor shape/dtype: ") + tt.name);
       if (!host.emplace(tt.name, tt.data).second)
         invalid(std::string("Duplicate AR tensor: ") + tt.name);
@@ -407,47 +462,103 @@ void build_engine(yuear_engine &E, const yuear_weight_source *src) {
     invalid("unknown weight source kind");
   }
 
-  // fetch one tensor as host bytes (borrowed or generated into `tmp`)
+  // one bf16 tensor as host bytes (borrowed, or generated into `buf`; the
+  // generator makes the bf16 values of a linear's `.weight` either way)
   std::vector<uint16_t> tmp, tmp2;
-  auto fetch = [&](const std::string &name, std::vector<uint16_t> &buf) -> const uint16_t * {
+  auto fetch = [&](const std::string &name, size_t n,
+                   std::vector<uint16_t> &buf) -> const uint16_t * {
     if (src->kind == YUEAR_WEIGHTS_HOST)
-      return host.at(name);
-    const size_t n = expected.at(name);
+      return static_cast<const uint16_t *>(host.at(name));
     buf.resize(n);
     const bool gain = name.find("norm") != std::string::npos;
     random_tensor(src->seed, tensor_id(name), gain ? 1.0f : 0.0f,
                   gain ? src->norm_std : src->std, int64_t(n), buf.data());
     return buf.data();
   };
-  auto upload = [&](uint16_t *dst, const uint16_t *h, size_t n) {
-    HIPC(hipMemcpy(dst, h, n * 2, hipMemcpyHostToDevice));
+  auto upload = [&](void *dst, const void *h, size_t bytes) {
+    HIPC(hipMemcpy(dst, h, bytes, hipMemcpyHostToDevice));
   };
-  upload(E.embed, fetch("model.embed_tokens.weight", tmp), Vs * Hs);
-  upload(E.lm_head, fetch("lm_head.weight", tmp), Vs * Hs);
-  upload(E.final_norm, fetch("model.norm.weight", tmp), Hs);
+  auto upload_bf16 = [&](uint16_t *dst, const std::string &name, size_t n) {
+    upload(dst, fetch(name, n, tmp), n * 2);
+  };
+  upload_bf16(E.embed, "model.embed_tokens.weight", Vs * Hs);
+  upload_bf16(E.final_norm, "model.norm.weight", Hs);
+
+  // A projection of `rows` x `k` built from parts: part p's source rows go
+  // to destination rows row0 + r * step (fused q|k|v rows; gate/up
+  // interleaved by row, 2r = gate_r, 2r + 1 = up_r, cuda_graph.py:100-108).
+  struct Part {
+    std::string weight;
+    size_t rows, row0, step;
+  };
+  std::vector<uint16_t> stage16;
+  std::vector<uint32_t> qstage, gstage, qgen;
+  std::vector<uint16_t> sgen, bgen;
+  auto put_linear = [&](const std::vector<Part> &parts, size_t total_rows, size_t k,
+                        uint16_t *dst, const uint32_t *dcodes, const uint32_t *dgroups) {
+    if (!bits) {
+      if (parts.size() == 1) {
+        upload(dst, fetch(parts[0].weight, total_rows * k, tmp), total_rows * k * 2);
+        return;
+      }
+      stage16.resize(total_rows * k);
+      for (const Part &pt : parts) {
+        const uint16_t *h = fetch(pt.weight, pt.rows * k, tmp);
+        for (size_t r = 0; r < pt.rows; ++r)
+          std::memcpy(&stage16[(pt.row0 + r * pt.step) * k], h + r * k, k * 2);
+      }
+      upload(dst, stage16.data(), stage16.size() * 2);
+      return;
+    }
+    const size_t wpr = k * bits / 32, gpr = k / 64;
+    qstage.resize(total_rows * wpr);
+    gstage.resize(total_rows * gpr);
+    for (const Part &pt : parts) {
+      const uint32_t *codes;
+      const uint16_t *scales, *biases;
+      const std::string base = base_of(pt.weight);
+      if (src->kind == YUEAR_WEIGHTS_HOST) {
+        codes = static_cast<const uint32_t *>(host.at(pt.weight));
+        scales = static_cast<const uint16_t *>(host.at(base + ".scales"));
+        biases = static_cast<const uint16_t *>(host.at(base + ".biases"));
+      } else {
+        const uint16_t *w = fetch(pt.weight, pt.rows * k, tmp);
+        qgen.resize(pt.rows * wpr);
+        sgen.resize(pt.rows * gpr);
+        bgen.resize(pt.rows * gpr);
+        quantize_affine(w, int64_t(pt.rows), int(k), bits, qgen.data(), sgen.data(), bgen.data());
+        codes = qgen.data();
+        scales = sgen.data();
+        biases = bgen.data();
+      }
+      for (size_t r = 0; r < pt.rows; ++r) {
+        const size_t d = pt.row0 + r * pt.step;
+        std::memcpy(&qstage[d * wpr], codes + r * wpr, wpr * 4);
+        for (size_t g = 0; g < gpr; ++g)
+          gstage[d * gpr + g] =
+              uint32_t(scales[r * gpr + g]) | (uint32_t(biases[r * gpr + g]) << 16);
+      }
+    }
+    upload(const_cast<uint32_t *>(dcodes), qstage.data(), qstage.size() * 4);
+    upload(const_cast<uint32_t *>(dgroups), gstage.data(), gstage.size() * 4);
+    HIPC(launch_dequantize(dcodes, dgroups, bits, int(total_rows), int(k), dst, nullptr));
+    HIPC(hipDeviceSynchronize());  // the staging buffers are reused
+  };
+  put_linear({{"lm_head.weight", Vs, 0, 1}}, Vs, Hs, E.lm_head, E.lm_q, E.lm_g);
   for (int i = 0; i < c.layers; ++i) {
     LayerW &L = E.layers[i];
-    upload(L.input_ln, fetch(layer_name(i, 0), tmp), Hs);
-    upload(L.post_ln, fetch(layer_name(i, 1), tmp), Hs);
-    upload(L.q_norm, fetch(layer_name(i, 2), tmp), c.D);
-    upload(L.k_norm, fetch(layer_name(i, 3), tmp), c.D);
-    // fused QKV rows: q | k | v (cuda_graph.py:100-108)
-    upload(L.qkv, fetch(layer_name(i, 4), tmp), QD * Hs);
-    upload(L.qkv + QD * Hs, fetch(layer_name(i, 5), tmp), KD * Hs);
-    upload(L.qkv + (QD + KD) * Hs, fetch(layer_name(i, 6), tmp), KD * Hs);
-    upload(L.o, fetch(layer_name(i, 7), tmp), Hs * QD);
-    // gate/up interleaved by row: 2r = gate_r, 2r + 1 = up_r
-    {
-      const uint16_t *g = fetch(layer_name(i, 8), tmp);
-      const uint16_t *u = fetch(layer_name(i, 9), tmp2);
-      std::vector<uint16_t> inter(2 * Fs * Hs);
-      for (size_t r = 0; r < Fs; ++r) {
-        std::memcpy(&inter[(2 * r) * Hs], g + r * Hs, Hs * 2);
-        std::memcpy(&inter[(2 * r + 1) * Hs], u + r * Hs, Hs * 2);
-      }
-      upload(L.gu, inter.data(), inter.size());
-    }
-    upload(L.down, fetch(layer_name(i, 10), tmp), Hs * Fs);
+    upload_bf16(L.input_ln, layer_name(i, 0), Hs);
+    upload_bf16(L.post_ln, layer_name(i, 1), Hs);
+    upload_bf16(L.q_norm, layer_name(i, 2), c.D);
+    upload_bf16(L.k_norm, layer_name(i, 3), c.D);
+    put_linear({{layer_name(i, 4), QD, 0, 1},
+                {layer_name(i, 5), KD, QD, 1},
+                {layer_name(i, 6), KD, QD + KD, 1}},
+               QD + 2 * KD, Hs, L.qkv, L.qqkv, L.gqkv);
+    put_linear({{layer_name(i, 7), Hs, 0, 1}}, Hs, QD, L.o, L.qo, L.go);
+    put_linear({{layer_name(i, 8), Fs, 0, 2}, {layer_name(i, 9), Fs, 1, 2}}, 2 * Fs, Hs, L.gu,
+               L.qgu, L.ggu);
+    put_linear({{layer_name(i, 10), Hs, 0, 1}}, Hs, Fs, L.down, L.qdown, L.gdown);
   }
   // RoPE tables for every position the model admits
   const int positions = std::min(c.max_pos, kContext);
@@ -455,8 +566,8 @@ void build_engine(yuear_engine &E, const yuear_weight_source *src) {
   rope_table(positions, c.D, c.theta, cs.data(), sn.data());
   HIPC(hipMalloc(&E.rope_cos, cs.size() * 4));
   E.rope_sin = E.rope_cos + cs.size();
-  upload(E.rope_cos, cs.data(), cs.size());
-  upload(E.rope_sin, sn.data(), sn.size());
+  upload(E.rope_cos, cs.data(), cs.size() * 2);
+  upload(E.rope_sin, sn.data(), sn.size() * 2);
 }
 
 // MFMA-tiled copies of every projection and the lm_head, for the batched
@@ -577,7 +688,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   // persistent decode step: needs every workgroup of its grid resident at
   // once; the grid is sized from the occupancy query (YUEAR_DECODE_WG_PER_CU
   // caps the workgroups per CU, default 2)
-  const int occ = decode_occupancy(c.H, c.F, c.Hq, c.Hkv, branches);
+  const int occ = E->bits ? 0 : decode_occupancy(c.H, c.F, c.Hq, c.Hkv, branches);
   if (occ > 0) {
     int cus = 0;
     HIPC(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, E->device));
@@ -626,7 +737,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   if (const char *env = std::getenv("YUEAR_FUSED_WAIT_US"))
     S.fused_ticks = std::max(0LL, std::atoll(env)) * 100;
   // fused layer kernel (1-2 branches)
-  S.fused_ok = fused_layer_supported(c.H, c.Hq, c.Hkv, c.D, branches);
+  S.fused_ok = E->bits == 0 && fused_layer_supported(c.H, c.Hq, c.Hkv, c.D, branches);
   if (S.fused_ok) {
     const size_t words = size_t(c.layers) * branches * (c.qkv() + c.Hq * c.D);
     S.fqkv = S.alloc<uint32_t>(words);  // zero words carry tag 0, which no step uses
@@ -651,6 +762,16 @@ void set_device_pos(yuear_session &S) {
   HIPC(hipStreamSynchronize(S.stream));
 }
 
+// Quantized codes of a projection: the 1-2 branch GEMVs read them instead
+// of the dequantized rows in `w`.
+void set_quant(GemvParams &g, int bits, const uint32_t *codes, const uint32_t *groups) {
+  if (bits && codes) {
+    g.bits = bits;
+    g.qw = codes;
+    g.qsb = groups;
+  }
+}
+
 // decode kernels of one layer on S.x (all branches)
 void enqueue_fused_qkv_attn_o(yuear_session &S, int l, bool embed_first);
 void enqueue_ffn(yuear_session &S, int l);
@@ -667,6 +788,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   }
   GemvParams q;
   q.w = L.qkv;
+  set_quant(q, E.bits, L.qqkv, L.gqkv);
   q.n = c.qkv();
   q.k = c.H;
   q.batch = S.B;
@@ -712,6 +834,7 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
 
   GemvParams o;
   o.w = L.o;
+  set_quant(o, E.bits, L.qo, L.go);
   o.n = c.H;
   o.k = c.Hq * c.D;
   o.batch = S.B;
@@ -734,6 +857,7 @@ void enqueue_ffn(yuear_session &S, int l) {
   hipStream_t st = S.stream;
   GemvParams g;
   g.w = L.gu;
+  set_quant(g, E.bits, L.qgu, L.ggu);
   g.n = 2 * c.F;
   g.k = c.H;
   g.batch = S.B;
@@ -750,6 +874,7 @@ void enqueue_ffn(yuear_session &S, int l) {
 
   GemvParams d;
   d.w = L.down;
+  set_quant(d, E.bits, L.qdown, L.gdown);
   d.n = c.H;
   d.k = c.F;
   d.batch = S.B;
@@ -833,6 +958,7 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   const Config &c = E.cfg;
   GemvParams h;
   h.w = E.lm_head;
+  set_quant(h, E.bits, E.lm_q, E.lm_g);
   h.n = S.phase.size;
   h.k = c.H;
   h.batch = batch;
@@ -864,17 +990,21 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
   g.eps = c.eps;
   if (which == "qkv") {
     g.w = L.qkv; g.n = c.qkv(); g.k = c.H; g.x = S.x; g.x_stride = c.H;
+    set_quant(g, E.bits, L.qqkv, L.gqkv);
     g.norm_w = L.input_ln; g.y = S.qkv; g.y_stride = c.qkv(); g.stage = S.stage;
     g.w_tiled = L.qkv_t;
   } else if (which == "o_proj") {
     g.w = L.o; g.n = c.H; g.k = c.Hq * c.D; g.x = S.attn; g.x_stride = c.Hq * c.D;
+    set_quant(g, E.bits, L.qo, L.go);
     g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual; g.w_tiled = L.o_t;
   } else if (which == "gate_up") {
     g.w = L.gu; g.n = 2 * c.F; g.k = c.H; g.x = S.x; g.x_stride = c.H;
+    set_quant(g, E.bits, L.qgu, L.ggu);
     g.norm_w = L.post_ln; g.y = S.act; g.y_stride = c.F; g.epilogue = kEpiSwiGLU;
     g.stage = S.stage; g.w_tiled = L.gu_t;
   } else if (which == "down") {
     g.w = L.down; g.n = c.H; g.k = c.F; g.x = S.act; g.x_stride = c.F;
+    set_quant(g, E.bits, L.qdown, L.gdown);
     g.y = S.x; g.y_stride = c.H; g.epilogue = kEpiResidual; g.w_tiled = L.down_t;
   } else if (which == "lm_head") {
     enqueue_head(S, S.x, S.B, c.H, S.logits, nullptr);
@@ -1197,6 +1327,16 @@ yuear_status yuear_engine_create(const yuear_model_config *config,
 
 void yuear_engine_destroy(yuear_engine *engine) { delete engine; }
 
+int32_t yuear_engine_bits(const yuear_engine *engine) { return engine ? engine->bits : -1; }
+
+void yuear_quantize_affine(const uint16_t *w, int64_t rows, int32_t k, int32_t bits,
+                           uint32_t *codes, uint16_t *scales, uint16_t *biases) {
+  if (!w || !codes || !scales || !biases || rows < 0 || k <= 0 || k % 64 ||
+      (bits != 4 && bits != 8))
+    return;
+  quantize_affine(w, rows, k, bits, codes, scales, biases);
+}
+
 void yuear_engine_cancel(yuear_engine *engine) {
   if (engine)
     engine->cancelled.store(true, std::memory_order_relaxed);
@@ -1354,6 +1494,9 @@ yuear_status yuear_session_set_decode_path(yuear_session *S, int32_t path, char 
                path != YUEAR_DECODE_FUSED))
       invalid("decode path must be YUEAR_DECODE_KERNELS, YUEAR_DECODE_PERSISTENT or "
               "YUEAR_DECODE_FUSED");
+    if (path != YUEAR_DECODE_KERNELS && S->e->bits)
+      invalid("the persistent and fused decode paths read bf16 weights; this engine's "
+              "linears are quantized");
     if (path == YUEAR_DECODE_PERSISTENT && !S->dsync)
       invalid("the persistent decode step is not available for this model shape / branch count");
     if (path == YUEAR_DECODE_FUSED && !S->fused_ok)
@@ -1767,6 +1910,32 @@ int32_t yuear_op_gemv(const uint16_t *w, int32_t n, int32_t k, int32_t batch, co
     return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
   }
   return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
+}
+
+int32_t yuear_op_qgemv(const uint32_t *codes, const uint32_t *groups, int32_t bits, int32_t n,
+                       int32_t k, int32_t batch, const uint16_t *x, int32_t x_stride,
+                       const uint16_t *norm_w, float eps, uint16_t *y, int32_t y_stride,
+                       int32_t epilogue, void *stream) {
+  GemvParams p;
+  p.qw = codes;
+  p.qsb = groups;
+  p.bits = bits;
+  p.n = n;
+  p.k = k;
+  p.batch = batch;
+  p.x = x;
+  p.x_stride = x_stride;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.y = y;
+  p.y_stride = y_stride;
+  p.epilogue = epilogue;
+  return int32_t(launch_qgemv(p, static_cast<hipStream_t>(stream)));
+}
+
+int32_t yuear_op_dequantize(const uint32_t *codes, const uint32_t *groups, int32_t bits, int32_t n,
+                            int32_t k, uint16_t *out, void *stream) {
+  return int32_t(launch_dequantize(codes, groups, bits, n, k, out, static_cast<hipStream_t>(stream)));
 }
 
 int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,

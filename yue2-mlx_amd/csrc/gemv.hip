@@ -64,6 +64,8 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t s) {
   if (p.k % 8 || p.k > 8192 || p.n < 1 || p.batch < 1 || p.batch > 8 ||
       (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2))
     return hipErrorInvalidValue;
+  if (p.bits && p.batch <= 2)  // quantized weights (qgemv.hip)
+    return launch_qgemv(p, s);
   if (gemv_mfma_supported(p))  // 3..8 rows: MFMA (gemv_mfma.hip)
     return launch_gemv_mfma(p, s);
   // Rows per wave. Batch 1: one row (QKV 5120 rows = 1280 workgroups, o_proj

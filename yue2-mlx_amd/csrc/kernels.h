@@ -42,8 +42,28 @@ struct GemvParams {
   // by the batched form when given (1 KiB contiguous per wave-load instead of
   // 16 row pieces of 64 bytes).
   const uint16_t *w_tiled = nullptr;
+  // Affine group-64 quantized weights (bits 8 or 4; 0: bf16 only): codes
+  // [rows][k * bits / 32] and one scale | bias << 16 word per group
+  // [rows][k / 64] (qgemv.hip). launch_gemv reads them for 1-2 branches;
+  // the batched form reads `w`, which then holds the dequantized rows.
+  const uint32_t *qw = nullptr;
+  const uint32_t *qsb = nullptr;
+  int bits = 0;
 };
 hipError_t launch_gemv(const GemvParams &p, hipStream_t s);
+// Quantized GEMV for 1-2 branches (qgemv.hip); k a multiple of 64 whose
+// pieces map onto 8..64 lanes per row.
+bool qgemv_supported(int bits, int k, int batch);
+hipError_t launch_qgemv(const GemvParams &p, hipStream_t s);
+// out [rows][k] = bf16(s q + b) of quantized rows (codes / group words as in
+// GemvParams::qw / qsb).
+hipError_t launch_dequantize(const uint32_t *codes, const uint32_t *sb, int bits, int rows, int k,
+                             uint16_t *out, hipStream_t s);
+// Host: affine group-64 quantization of bf16 rows [rows][k] into codes
+// [rows][k * bits / 32] and bf16 scales / biases [rows][k / 64]
+// (quantize.hip).
+void quantize_affine(const uint16_t *w, int64_t rows, int k, int bits, uint32_t *codes,
+                     uint16_t *scales, uint16_t *biases);
 // MFMA form for 3..8 independent rows (batched sequences); launch_gemv
 // dispatches to it when gemv_mfma_supported(p).
 bool gemv_mfma_supported(const GemvParams &p);

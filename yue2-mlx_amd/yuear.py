@@ -26,7 +26,9 @@ if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C yue2-mlx_amd)")
 
 u16p = C.POINTER(C.c_uint16)
+u32p = C.POINTER(C.c_uint32)
 i32p = C.POINTER(C.c_int32)
+DTYPE_BF16, DTYPE_U32 = 0, 1  # YUEAR_DTYPE_*
 
 
 class ModelConfig(C.Structure):
@@ -44,12 +46,14 @@ class SamplingC(C.Structure):
 
 
 class TensorC(C.Structure):
-    _fields_ = [("name", C.c_char_p), ("data", u16p), ("numel", C.c_int64)]
+    _fields_ = [("name", C.c_char_p), ("data", C.c_void_p), ("numel", C.c_int64),
+                ("dtype", C.c_int32)]
 
 
 class WeightSource(C.Structure):
     _fields_ = [("kind", C.c_int32), ("seed", C.c_uint64), ("std", C.c_float),
-                ("norm_std", C.c_float), ("tensors", C.POINTER(TensorC)), ("count", C.c_int32)]
+                ("norm_std", C.c_float), ("tensors", C.POINTER(TensorC)), ("count", C.c_int32),
+                ("bits", C.c_int32)]
 
 
 TOKEN_CB = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int32)
@@ -67,6 +71,8 @@ _SIGS = {
     "yuear_engine_load": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int32, _P(C.c_void_p),
                                     _P(C.c_void_p)]),
     "yuear_engine_cancel": (None, [C.c_void_p]),
+    "yuear_engine_bits": (C.c_int32, [C.c_void_p]),
+    "yuear_quantize_affine": (None, [u16p, C.c_int64, C.c_int32, C.c_int32, u32p, u16p, u16p]),
     "yuear_tensor_id": (C.c_int32, [C.c_char_p]),
     "yuear_random_tensor": (None, [C.c_uint64, C.c_int32, C.c_float, C.c_float, C.c_int64,
                                    u16p]),
@@ -110,6 +116,11 @@ _SIGS = {
                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                               C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                               C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    "yuear_op_qgemv": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                   C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_float,
+                                   C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
+    "yuear_op_dequantize": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                        C.c_int32, C.c_void_p, C.c_void_p]),
     "yuear_op_gemm": (C.c_int32, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                   C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
     "yuear_op_attention_prefill": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
@@ -192,6 +203,34 @@ def random_normal(seed, tensor_id, shape, mean=0.0, std=1.0):
     """Generator bytes for an arbitrary stream id (inputs such as KV caches)."""
     out = np.empty(shape, dtype=np.uint16)
     lib.yuear_random_tensor(seed, tensor_id, mean, std, out.size, out.ctypes.data_as(u16p))
+    return out
+
+
+def quantize_affine(w, bits):
+    """bf16 rows [rows][k] -> (uint32 codes [rows][k * bits / 32], bf16 scales
+    and biases [rows][k / 64]) as the engine's RANDOM source quantizes them
+    (mx::quantize(w, 64, bits, "affine"), conversion.cpp:508)."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    rows, k = w.shape
+    codes = np.empty((rows, k * bits // 32), dtype=np.uint32)
+    scales = np.empty((rows, k // 64), dtype=np.uint16)
+    biases = np.empty_like(scales)
+    lib.yuear_quantize_affine(w.ctypes.data_as(u16p), rows, k, bits, codes.ctypes.data_as(u32p),
+                              scales.ctypes.data_as(u16p), biases.ctypes.data_as(u16p))
+    return codes, scales, biases
+
+
+def quantized_weights(weights, bits):
+    """The weight dict of the "8bit" / "4bit" precision made from a bf16 one:
+    every projection and the lm_head through `quantize_affine` (ar.cpp:209-214),
+    the embedding and the norms unchanged."""
+    out = {}
+    for name, value in weights.items():
+        base = name[:-len(".weight")]
+        if base == "lm_head" or base.endswith("_proj"):
+            out[name], out[base + ".scales"], out[base + ".biases"] = quantize_affine(value, bits)
+        else:
+            out[name] = value
     return out
 
 
@@ -281,20 +320,26 @@ class Engine:
     """ARModel equivalent: device weights for one config (ar.cpp:133-245)."""
 
     def __init__(self, config: dict, weights: dict | None = None, *, seed=0, std=0.02,
-                 norm_std=0.0):
+                 norm_std=0.0, bits=0):
+        """bits 8 / 4: affine group-64 quantized linears (the "8bit" / "4bit"
+        precisions): `weights` then holds uint32 codes for every `*_proj` /
+        `lm_head` `.weight` plus bf16 `.scales` / `.biases`; without weights
+        the random bf16 linears are quantized by `quantize_affine`."""
         self.config = dict(config)
         self._cfg = _config_struct(self.config)
         keep = []
         if weights is None:
-            src = WeightSource(0, seed, std, norm_std, None, 0)
+            src = WeightSource(0, seed, std, norm_std, None, 0, bits)
         else:
             table = (TensorC * len(weights))()
             for i, (name, arr) in enumerate(weights.items()):
-                arr = np.ascontiguousarray(arr, dtype=np.uint16)
+                u32 = np.asarray(arr).dtype == np.uint32
+                arr = np.ascontiguousarray(arr, dtype=np.uint32 if u32 else np.uint16)
                 keep.append(arr)
-                table[i] = TensorC(name.encode(), arr.ctypes.data_as(u16p), arr.size)
+                table[i] = TensorC(name.encode(), arr.ctypes.data, arr.size,
+                                   DTYPE_U32 if u32 else DTYPE_BF16)
             keep.append(table)
-            src = WeightSource(1, 0, 0.0, 0.0, table, len(weights))
+            src = WeightSource(1, 0, 0.0, 0.0, table, len(weights), bits)
         handle = C.c_void_p()
         err = C.c_void_p()
         _check(lib.yuear_engine_create(C.byref(self._cfg), C.byref(src), C.byref(handle),
@@ -325,6 +370,11 @@ class Engine:
 
     def cancel(self):
         lib.yuear_engine_cancel(self.handle)
+
+    @property
+    def bits(self):
+        """0 for bf16 linears, else the quantization bits."""
+        return lib.yuear_engine_bits(self.handle)
 
     def session(self, branches=1, capacity=1024, phase="full"):
         return Session(self, branches, capacity, phase)
