@@ -291,6 +291,36 @@ int32_t yuear_op_attention_prefill(const uint16_t *dev_q,
                                    int32_t pos0, int32_t heads,
                                    int32_t kv_heads, int32_t capacity,
                                    uint16_t *dev_out, void *stream);
+/* Acoustic-model attention: the drop-in for nar_attention(query, key, value,
+ * causal, query_chunk_size) (nar_attention.cpp:224-270) and its Metal kernel
+ * lyra_nar_precise_attention (nar_attention.cpp:63-218). q [batch][heads]
+ * [q_len][head_dim], k / v [batch][kv_heads][kv_len][head_dim], out like q,
+ * all bf16; query head h reads kv head h / (heads / kv_heads). fp32 scores
+ * times scale * log2(e), exp2 softmax, fp32 P.V, bf16(o / l); causal hides
+ * the keys after each query (q_len == kv_len). query_chunk_size is validated
+ * as in the reference and does not change the result (every query sees the
+ * same keys in one pass). workspace: yuear_nar_attention_workspace_bytes()
+ * of device memory. Runs on `stream` (a hipStream_t, NULL = default); the
+ * reference's ValueError messages for invalid shapes. */
+int64_t yuear_nar_attention_workspace_bytes(int32_t batch, int32_t kv_heads, int32_t kv_len);
+/* The acoustic stage's conditioning prefill (CachedNAR, nar.cpp:139-190):
+ * the AR layers over `tokens` with causal attention (the engine's prefill;
+ * nar.cpp:80-99 keeps ar.cpp's RoPE and rounding points), then each layer's
+ * keys and values of positions [0, visible), visible = visible_end ?
+ * min(visible_end, n) : n, written to device memory dev_k / dev_v
+ * [layers][kv_heads][visible][head_dim] bf16 (per layer the [1, heads,
+ * tokens, dim] tensors yuear_nar_attention takes). *visible_out receives
+ * visible. Errors as nar.cpp:142-154 (ValueError); engines with quantized
+ * linears cannot condition (nar.cpp:303-307). */
+yuear_status yuear_nar_condition(yuear_engine *engine, const int32_t *tokens, int32_t n,
+                                 int32_t visible_end, uint16_t *dev_k, uint16_t *dev_v,
+                                 int32_t *visible_out, char **error_json);
+yuear_status yuear_nar_attention(const uint16_t *dev_q, const uint16_t *dev_k,
+                                 const uint16_t *dev_v, int32_t batch, int32_t heads,
+                                 int32_t kv_heads, int32_t q_len, int32_t kv_len,
+                                 int32_t head_dim, int32_t causal, int32_t query_chunk_size,
+                                 void *dev_workspace, uint16_t *dev_out, void *stream,
+                                 char **error_json);
 /* RoPE cos/sin tables exactly as the engine builds them (host). */
 void yuear_rope_table(int32_t positions, int32_t head_dim, double theta,
                       uint16_t *cos_out, uint16_t *sin_out);

@@ -427,6 +427,49 @@ void oracle_attention(const uint16_t *q, const uint16_t *keys,
     }
 }
 
+// The acoustic model's attention (nar_attention.cpp:224-270): q [B][Hq][Lq][D],
+// keys / values [B][Hkv][Lk][D] (the [batch, heads, tokens, dim] tensors),
+// query head h reads kv head h / (Hq / Hkv). Restated from the non-causal
+// kernel lyra_nar_precise_attention (nar_attention.cpp:63-218): fp32 scores
+// of the bf16 operands, times scale * log2(e) as one fp32 constant, exp2
+// softmax in fp32, fp32 P times bf16 V summed in fp32, bf16(o / l). causal
+// (Lq == Lk, the conditioning prefill, nar.cpp:176) hides keys after the
+// query's own position.
+void oracle_nar_attention(const uint16_t *q, const uint16_t *keys, const uint16_t *values,
+                          int B, int Hq, int Hkv, int Lq, int Lk, int D, int causal,
+                          uint16_t *out) {
+  const int group = Hq / Hkv;
+  const float scale2 = float(std::pow(double(D), -0.5)) * 1.4426950408889634f;
+#pragma omp parallel for collapse(3) schedule(dynamic)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h)
+      for (int t = 0; t < Lq; ++t) {
+        const int kvh = h / group, L = causal ? t + 1 : Lk;
+        const uint16_t *K = keys + (size_t(b) * Hkv + kvh) * Lk * D;
+        const uint16_t *V = values + (size_t(b) * Hkv + kvh) * Lk * D;
+        const uint16_t *qr = q + ((size_t(b) * Hq + h) * Lq + t) * D;
+        std::vector<float> qs(D), sc(L), acc(D, 0.f);
+        for (int d = 0; d < D; ++d)
+          qs[d] = bf2f(qr[d]);
+        float m = -std::numeric_limits<float>::infinity();
+        for (int j = 0; j < L; ++j) {
+          sc[j] = dot_f32_bf16(qs.data(), K + size_t(j) * D, D) * scale2;
+          m = std::max(m, sc[j]);
+        }
+        float l = 0.f;
+        for (int j = 0; j < L; ++j) {
+          const float p = std::exp2(sc[j] - m);
+          l += p;
+          const uint16_t *vr = V + size_t(j) * D;
+          for (int d = 0; d < D; ++d)
+            acc[d] += p * bf2f(vr[d]);
+        }
+        uint16_t *o = out + ((size_t(b) * Hq + h) * Lq + t) * D;
+        for (int d = 0; d < D; ++d)
+          o[d] = f2bf(acc[d] / l);
+      }
+}
+
 // ---- model / cache ----
 
 oracle_model *oracle_model_new(const oracle_config *c, const oracle_weights *w) {

@@ -32,6 +32,9 @@
  *   silu_mul ...................... reference test_ar.py known answers
  *   attention ..................... fp64 brute force; split-merge identity;
  *                                   causal chunk == full
+ *   nar_attention ................. fp64 brute force; key permutation
+ *                                   invariance; causal == the AR prefill
+ *                                   attention; equal keys give the mean of V
  *   layer / model composition ..... golden vectors from the upstream torch model
  *   guided_logits ................. reference test_sampling.py known answers
  *   distribution .................. reference test_sampling.py / test_fast.py
@@ -124,6 +127,12 @@ void oracle_silu_mul(const uint16_t *g, const uint16_t *u, int n,
 void oracle_attention(const uint16_t *q, const uint16_t *keys,
                       const uint16_t *values, int T, int Hq, int Hkv, int D,
                       int cap, int offset, uint16_t *out);
+/* nar_attention (nar_attention.cpp:63-270): q [B][Hq][Lq][D], keys/values
+ * [B][Hkv][Lk][D], out [B][Hq][Lq][D]; fp32 scores times scale * log2(e),
+ * exp2 softmax, fp32 P.V, bf16(o / l); causal needs Lq == Lk. */
+void oracle_nar_attention(const uint16_t *q, const uint16_t *keys, const uint16_t *values,
+                          int B, int Hq, int Hkv, int Lq, int Lk, int D, int causal,
+                          uint16_t *out);
 void oracle_rope_table(int positions, int d, double theta, uint16_t *cos_out,
                        uint16_t *sin_out);
 

@@ -76,6 +76,8 @@ def _load():
         "oracle_silu_mul": (None, [u16p, u16p, C.c_int, u16p]),
         "oracle_attention": (None, [u16p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int,
                                     C.c_int, C.c_int, u16p]),
+        "oracle_nar_attention": (None, [u16p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_int, u16p]),
         "oracle_model_new": (C.c_void_p, [C.POINTER(Config), C.POINTER(Weights)]),
         "oracle_model_new_quantized": (C.c_void_p, [C.POINTER(Config), C.POINTER(Weights),
                                                     C.POINTER(Quant)]),
@@ -213,6 +215,20 @@ def attention(q, keys, values, offset):
     Hkv, cap, _ = keys.shape
     out = np.empty((T, Hq * D), dtype=np.uint16)
     lib().oracle_attention(pq, pk, pv, T, Hq, Hkv, D, cap, offset, out.ctypes.data_as(u16p))
+    return out
+
+
+def nar_attention(q, keys, values, causal=False):
+    """q [B, Hq, Lq, D]; keys/values [B, Hkv, Lk, D] -> [B, Hq, Lq, D]
+    (nar_attention.cpp:63-270)."""
+    q, pq = _u16(q)
+    keys, pk = _u16(keys)
+    values, pv = _u16(values)
+    B, Hq, Lq, D = q.shape
+    _, Hkv, Lk, _ = keys.shape
+    out = np.empty_like(q)
+    lib().oracle_nar_attention(pq, pk, pv, B, Hq, Hkv, Lq, Lk, D, int(causal),
+                               out.ctypes.data_as(u16p))
     return out
 
 

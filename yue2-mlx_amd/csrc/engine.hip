@@ -1938,6 +1938,94 @@ int32_t yuear_op_dequantize(const uint32_t *codes, const uint32_t *groups, int32
   return int32_t(launch_dequantize(codes, groups, bits, n, k, out, static_cast<hipStream_t>(stream)));
 }
 
+yuear_status yuear_nar_condition(yuear_engine *E, const int32_t *tokens, int32_t n,
+                                 int32_t visible_end, uint16_t *dev_k, uint16_t *dev_v,
+                                 int32_t *visible_out, char **error_json) {
+  if (visible_out)
+    *visible_out = 0;
+  return guarded(error_json, [&] {
+    if (!E || !dev_k || !dev_v)
+      invalid("engine and output buffers are required");
+    std::unique_lock<std::mutex> lock(E->busy, std::try_to_lock);
+    if (!lock.owns_lock())
+      throw Error("RuntimeError", "This engine is already executing an operation");
+    E->cancelled.store(false, std::memory_order_relaxed);
+    const Config &c = E->cfg;
+    // nar.cpp:142-154, 303-307
+    if (E->bits)
+      invalid("Shared AR tensors must be BF16; quantized AR cannot condition NAR");
+    if (!tokens || n < 1)
+      invalid("AR conditioning tokens are outside the model vocabulary");
+    for (int i = 0; i < n; ++i)
+      if (tokens[i] < 0 || tokens[i] >= c.V)
+        invalid("AR conditioning tokens are outside the model vocabulary");
+    if (visible_end < 0)
+      invalid("nar_cond_end must be a nonnegative integer");
+    if (n > std::min(kContext, c.max_pos))
+      invalid("AR conditioning tokens exceed the model context");
+    const int visible = visible_end ? std::min(visible_end, n) : n;
+    auto S = std::make_unique<yuear_session>();
+    begin_session(*S, E, 1, n, "full");
+    prefill(*S, 0, tokens, n, nullptr);
+    // per layer: keys / values of positions [0, visible), [Hkv][visible][D]
+    const size_t per_layer = size_t(c.Hkv) * visible * c.D;
+    for (int l = 0; l < c.layers; ++l) {
+      const size_t off = S->layer_kv_offset(l, 0);
+      HIPC(hipMemcpy2DAsync(dev_k + l * per_layer, size_t(visible) * c.D * 2, S->kc + off,
+                            size_t(S->kv_stride) * c.D * 2, size_t(visible) * c.D * 2, c.Hkv,
+                            hipMemcpyDeviceToDevice, S->stream));
+      HIPC(launch_v_rows(S->vc + off, S->kv_stride, c.Hkv, visible, dev_v + l * per_layer,
+                         S->stream));
+    }
+    HIPC(hipStreamSynchronize(S->stream));
+    if (visible_out)
+      *visible_out = visible;
+  });
+}
+
+int64_t yuear_nar_attention_workspace_bytes(int32_t batch, int32_t kv_heads, int32_t kv_len) {
+  if (batch < 1 || kv_heads < 1 || kv_len < 1)
+    return 0;
+  return int64_t(nar_attention_workspace_elems(batch, kv_heads, kv_len) * 2);
+}
+
+yuear_status yuear_nar_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                 int32_t batch, int32_t heads, int32_t kv_heads, int32_t q_len,
+                                 int32_t kv_len, int32_t head_dim, int32_t causal,
+                                 int32_t query_chunk_size, void *workspace, uint16_t *out,
+                                 void *stream, char **error_json) {
+  return guarded(error_json, [&] {
+    // nar_attention.cpp:227-243
+    if (batch < 1 || head_dim < 1)
+      invalid("Expected attention Q/K/V shaped [batch,heads,tokens,dim]");
+    if (kv_heads < 1 || heads < 1 || heads % kv_heads)
+      invalid("Invalid grouped-query head count");
+    if (q_len < 1 || kv_len < 1)
+      invalid("Attention sequences must be nonempty");
+    if (causal && q_len != kv_len)
+      invalid("Causal prefill requires equal query and key lengths");
+    if (query_chunk_size < 1)
+      invalid("query_chunk_size must be a positive integer");
+    if (head_dim != 128)
+      invalid("the gfx950 kernels implement head_dim 128");
+    if (!q || !k || !v || !workspace || !out)
+      invalid("device buffers are required");
+    NarAttnParams p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.vb = static_cast<uint16_t *>(workspace);
+    p.out = out;
+    p.batch = batch;
+    p.heads = heads;
+    p.kv_heads = kv_heads;
+    p.q_len = q_len;
+    p.kv_len = kv_len;
+    p.causal = causal != 0;
+    HIPC(launch_nar_attention(p, static_cast<hipStream_t>(stream)));
+  });
+}
+
 int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
                                   const uint16_t *k_norm, float eps, const uint16_t *rope_cos,
                                   const uint16_t *rope_sin, uint16_t *k_cache, uint16_t *v_cache,

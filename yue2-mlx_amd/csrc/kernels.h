@@ -134,6 +134,24 @@ struct FusedLayerParams {
 bool fused_layer_supported(int hidden, int heads, int kv_heads, int head_dim, int batch);
 hipError_t launch_fused_layer(FusedLayerParams p, hipStream_t s);
 
+// Acoustic-model attention (nar_attention.hip, nar_attention.cpp:63-270):
+// q [batch][heads][q_len][128], k / v [batch][kv_heads][kv_len][128], out
+// like q; vb: workspace of nar_attention_workspace_elems() bf16 (V in 32-key
+// dim-major blocks). causal needs q_len == kv_len.
+struct NarAttnParams {
+  const uint16_t *q = nullptr, *k = nullptr, *v = nullptr;
+  uint16_t *vb = nullptr;
+  uint16_t *out = nullptr;
+  int batch = 1, heads = 0, kv_heads = 0, q_len = 0, kv_len = 0, causal = 0;
+  int kv_pad = 0;  // set by launch_nar_attention: kv_len rounded up to 32
+};
+size_t nar_attention_workspace_elems(int batch, int kv_heads, int kv_len);
+// Keys [0, n) of `heads` cache heads (V in 32-key dim-major blocks, heads
+// kv_stride slots apart) to row-major out [heads][n][128].
+hipError_t launch_v_rows(const uint16_t *vb, int kv_stride, int heads, int n, uint16_t *out,
+                         hipStream_t s);
+hipError_t launch_nar_attention(NarAttnParams p, hipStream_t s);
+
 // Device sampler: CFG merge + distribution() + draw, one token per call.
 struct SamplerParams {
   const uint16_t *logits = nullptr;  // [branches][ls] phase-local bf16

@@ -121,6 +121,13 @@ _SIGS = {
                                    C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
     "yuear_op_dequantize": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                         C.c_int32, C.c_void_p, C.c_void_p]),
+    "yuear_nar_attention_workspace_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32]),
+    "yuear_nar_condition": (C.c_int, [C.c_void_p, i32p, C.c_int32, C.c_int32, C.c_void_p,
+                                      C.c_void_p, i32p, _P(C.c_void_p)]),
+    "yuear_nar_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                      C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                      C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      _P(C.c_void_p)]),
     "yuear_op_gemm": (C.c_int32, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                   C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
     "yuear_op_attention_prefill": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
@@ -203,6 +210,25 @@ def random_normal(seed, tensor_id, shape, mean=0.0, std=1.0):
     """Generator bytes for an arbitrary stream id (inputs such as KV caches)."""
     out = np.empty(shape, dtype=np.uint16)
     lib.yuear_random_tensor(seed, tensor_id, mean, std, out.size, out.ctypes.data_as(u16p))
+    return out
+
+
+def nar_attention(q, k, v, causal=False, query_chunk_size=64, workspace=None, stream=None):
+    """nar_attention(query, key, value, causal, query_chunk_size)
+    (nar_attention.cpp:224-270) on device tensors: q [B, Hq, Lq, 128], k / v
+    [B, Hkv, Lk, 128], torch bf16 on the GPU (plumbing only; the work is
+    libyuear's kernel). Returns the output tensor (q's shape)."""
+    import torch
+    B, Hq, Lq, Dh = q.shape
+    _, Hkv, Lk, _ = k.shape
+    out = torch.empty_like(q)
+    if workspace is None:
+        nbytes = lib.yuear_nar_attention_workspace_bytes(B, Hkv, Lk)
+        workspace = torch.empty(max(nbytes, 2) // 2, dtype=torch.bfloat16, device=q.device)
+    err = C.c_void_p()
+    _check(lib.yuear_nar_attention(q.data_ptr(), k.data_ptr(), v.data_ptr(), B, Hq, Hkv, Lq, Lk,
+                                   Dh, int(causal), int(query_chunk_size), workspace.data_ptr(),
+                                   out.data_ptr(), stream, C.byref(err)), err)
     return out
 
 
@@ -370,6 +396,25 @@ class Engine:
 
     def cancel(self):
         lib.yuear_engine_cancel(self.handle)
+
+    def nar_condition(self, tokens, visible_end=0):
+        """CachedNAR's conditioning prefill (nar.cpp:139-190): per layer the keys
+        and values of the visible prefix, as torch bf16 device tensors
+        [layers, kv_heads, visible, 128] (plumbing; the work is libyuear's)."""
+        import torch
+        c = self.config
+        ids = _i32(tokens)
+        n = len(ids)
+        visible = min(visible_end, n) if visible_end else n
+        shape = (c["num_hidden_layers"], c["num_key_value_heads"], max(visible, 1), 128)
+        k = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+        v = torch.empty_like(k)
+        got = C.c_int32()
+        err = C.c_void_p()
+        _check(lib.yuear_nar_condition(self.handle, ids.ctypes.data_as(i32p), n, int(visible_end),
+                                       k.data_ptr(), v.data_ptr(), C.byref(got), C.byref(err)),
+               err)
+        return k[:, :, :got.value], v[:, :, :got.value]
 
     @property
     def bits(self):
