@@ -176,6 +176,51 @@ def run_long(args, engine, c):
             "mfma_frac": round(flops / pre_s / PEAK_BF16, 4), "decode_curve": curve}
 
 
+def run_nar(args):
+    """The acoustic-model attention (nar_attention.cpp:63-218) at the 3B head
+    shape: a 512-frame chunk attending over 3000 conditioning keys plus its
+    own (non-causal), and the causal form over 3000 tokens."""
+    import torch
+    import yuear
+    Hq, Hkv, D = 24, 8, 128
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    out = {}
+    for name, Lq, Lk, causal in (("chunk", 512, 3512, False), ("causal", 3000, 3000, True)):
+        q = torch.randn(1, Hq, Lq, D, device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn(1, Hkv, Lk, D, device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn(1, Hkv, Lk, D, device="cuda", generator=g).to(torch.bfloat16)
+        ws = torch.empty(yuear.lib.yuear_nar_attention_workspace_bytes(1, Hkv, Lk) // 2,
+                         dtype=torch.bfloat16, device="cuda")
+        stream = torch.cuda.current_stream()
+        for _ in range(3):
+            yuear.nar_attention(q, k, v, causal, workspace=ws, stream=stream.cuda_stream)
+        reps = 20
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            yuear.nar_attention(q, k, v, causal, workspace=ws, stream=stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        pairs = Lq * (Lq + 1) // 2 if causal else Lq * Lk  # visible (query, key) pairs
+        flops = 4 * pairs * D * Hq
+        out[name] = {"q_len": Lq, "kv_len": Lk, "causal": causal, "ms": round(ms, 4),
+                     "TFLOPs": round(flops / (ms / 1e3) / 1e12, 1),
+                     "frac_bf16_peak": round(flops / (ms / 1e3) / PEAK_BF16, 4)}
+        log(f"[bench] nar {name}: {Lq} x {Lk} causal={causal} {ms:.3f} ms "
+            f"{flops / (ms / 1e3) / 1e12:.1f} TFLOP/s")
+    return {"metric": "acoustic-model attention TFLOP/s (nar_attention, 3B heads 24/8)",
+            "value": out["chunk"]["TFLOPs"], "unit": "TFLOP/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "bf16 (fp32 softmax and P.V)",
+            "data": "synthetic N(0,1) q/k/v",
+            "config": {"workload": "nar_attention: 512-query chunk over 3512 keys; causal 3000"},
+            "roofline": {"bound": "mfma", "achieved": out["chunk"]["TFLOPs"],
+                         "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                         "frac": out["chunk"]["frac_bf16_peak"], "traffic": None},
+            "shapes": out}
+
+
 def run_batch8(args, engine, c):
     import numpy as np
     import torch
@@ -283,7 +328,8 @@ def main():
     ap.add_argument("--decode", choices=("kernels", "fused", "persistent"), default="kernels",
                     help="decode step: one kernel per op, a fused QKV+attention+o_proj "
                          "launch per layer, or one persistent kernel")
-    ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8"), default="decode",
+    ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8", "nar"),
+                    default="decode",
                     help="workload (decode: the headline batch-1 KV-4096 line)")
     ap.add_argument("--phase-trace", action="store_true",
                     help="profiling mode: per-phase timeline of one persistent decode step")
@@ -313,6 +359,9 @@ def main():
         return
 
     t_start = time.perf_counter()
+    if args.config == "nar":
+        print(json.dumps(run_nar(args)), flush=True)
+        return
     c = CONFIG
     bits = precision_bits(args)
     log(f"[bench] generating 3B weights on host ({weight_bytes(c) / 1e9:.2f} GB) ...")

@@ -10,6 +10,7 @@
 #include <cmath>
 
 #include "attn_core.h"
+#include "attn_tile.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -332,141 +333,30 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
 
 // ---------------------------------------------------------------------------
 // Causal attention on MFMA (ar.cpp:284-291: fp32 scores, softmax and P.V,
-// bf16 output). Workgroup = 4 independent waves on one q head; wave w owns
-// queries q0 = 128 blockIdx.y' + 32 w + [0, 32) as two 16-query MFMA column
-// tiles and walks the 32-key V blocks of its causal range [0, pos0 + last
-// query], one block per step with the next block's K/V loads in flight:
-//
-//   S^T[key][query] = K[key][:] . q[query][:]     (attn_core.h row order)
-//   O^T[dim][query] += V^T[dim][key] . P^T[key][query]   P as hi + mid + lo
-//
-// the decode core's arithmetic with the queries as MFMA columns. Products
-// are exact and all sums fp32; the output is bf16(o / l) as in the
-// reference. Query tiles are dispatched longest first (the causal tail), and
-// all heads of a tile run together so K/V blocks are shared in L2.
+// bf16 output): one workgroup per (q head, 32-query tile), the tile's keys
+// [0, pos0 + last query] split over the 4 waves and merged in LDS
+// (attn_tile.h). Query t sits at position pos0 + t. Tiles are dispatched
+// longest causal range first, and all heads of a tile run together so the
+// K/V blocks are shared in L2.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
+  __shared__ attn::TileLds sh;
   using attn::D;
-  using attn::f32x4;
-  using attn::kBlock;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane >> 4, i = lane & 15;
   const int h = blockIdx.x;
   const int tile = gridDim.y - 1 - blockIdx.y;  // longest causal range first
-  const int qbase = tile * 128 + wave * 32;
-  if (qbase >= p.tokens)
-    return;  // whole wave idle (no barriers in this kernel)
+  const int q0 = tile * 32;
   const int kvh = h / (p.heads / p.kv_heads);
-  const int kend = p.pos0 + min(qbase + 32, p.tokens);  // keys [0, kend)
-  const int last = kend - 1;
-  const u32x4 *kc = reinterpret_cast<const u32x4 *>(p.k_cache) + size_t(kvh) * p.capacity * (D / 8);
-  const u32x4 *vc = reinterpret_cast<const u32x4 *>(p.v_cache) + size_t(kvh) * p.capacity * (D / 8);
-
-  // Q^T operands: column tile c, query qbase + 16 c + i (clamped), dims 32 s + 8 r
-  u32x4 qb[2][4];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int qi = min(qbase + 16 * c + i, p.tokens - 1);
-    const u32x4 *src = reinterpret_cast<const u32x4 *>(p.q + (size_t(qi) * p.heads + h) * D);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      qb[c][s] = src[4 * s + r];
-  }
-  u32x4 kr[8], vr[8];
-  attn::load_k(kc, 0, 0, lane, last, kr);
-  attn::load_v(vc, 0, 0, lane, last, vr);
-
-  float m_run[2] = {-__builtin_inff(), -__builtin_inff()}, l_run[2] = {0.f, 0.f};
-  f32x4 o[2][8];
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      o[c][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int kb = 0; kb < kend; kb += kBlock) {
-    const bool more = kb + kBlock < kend;  // uniform
-    u32x4 kn[8], vn[8];
-    if (more) {
-      attn::load_k(kc, kb + kBlock, 0, lane, last, kn);
-      attn::load_v(vc, kb + kBlock, 0, lane, last, vn);
-    }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      f32x4 st[2];
-#pragma unroll
-      for (int T = 0; T < 2; ++T) {
-        st[T] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          st[T] = attn::mfma(kr[4 * T + s], qb[c][s], st[T]);
-      }
-      // lane (query qbase + 16 c + i, r): keys kb + 8 r + 4 T + t, visible up
-      // to the query's own position pos0 + q
-      const int qpos = p.pos0 + qbase + 16 * c + i;
-      float sc[8];
-#pragma unroll
-      for (int T = 0; T < 2; ++T)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          sc[4 * T + t] = kb + 8 * r + 4 * T + t <= qpos ? st[T][t] * qscale : -__builtin_inff();
-      float mx = sc[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e)
-        mx = fmaxf(mx, sc[e]);
-      mx = max_halves(max_row_pairs(mx));
-      const float m_new = fmaxf(m_run[c], mx);
-      const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
-      const float corr = __builtin_amdgcn_exp2f(m_run[c] - m_use);
-      float ps = 0.f;
-      uint32_t pw[3][4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float p0 = __builtin_amdgcn_exp2f(sc[2 * q] - m_use);
-        float p1 = __builtin_amdgcn_exp2f(sc[2 * q + 1] - m_use);
-        ps += p0;
-        ps += p1;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          const uint16_t b0 = f2bf(p0), b1 = f2bf(p1);
-          pw[k][q] = uint32_t(b0) | (uint32_t(b1) << 16);
-          p0 -= bf2f(b0);
-          p1 -= bf2f(b1);
-        }
-      }
-      l_run[c] = l_run[c] * corr + ps;
-      m_run[c] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        o[c][dt] *= corr;
-#pragma unroll
-        for (int k = 0; k < 3; ++k)
-          o[c][dt] = attn::mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[c][dt]);
-      }
-    }
-    if (more) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kr[j] = kn[j];
-        vr[j] = vn[j];
-      }
-    }
-  }
-  // lane (query, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const float l = sum_halves(sum_row_pairs(l_run[c]));
-    const int qi = qbase + 16 * c + i;
-    if (qi < p.tokens) {
-      uint16_t *dst = p.out + size_t(qi) * p.heads * D + size_t(h) * D;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint32_t lo = uint32_t(f2bf(o[c][dt][0] / l)) | (uint32_t(f2bf(o[c][dt][1] / l)) << 16);
-        const uint32_t hi = uint32_t(f2bf(o[c][dt][2] / l)) | (uint32_t(f2bf(o[c][dt][3] / l)) << 16);
-        *reinterpret_cast<uint2 *>(dst + 16 * dt + 4 * r) = uint2{lo, hi};
-      }
-    }
-  }
+  attn::QueryTile t;
+  t.kc = reinterpret_cast<const u32x4 *>(p.k_cache) + size_t(kvh) * p.capacity * (D / 8);
+  t.vc = reinterpret_cast<const u32x4 *>(p.v_cache) + size_t(kvh) * p.capacity * (D / 8);
+  t.nq = min(32, p.tokens - q0);
+  t.kend = p.pos0 + q0 + t.nq;
+  t.causal_pos = p.pos0 + q0;
+  t.q = p.q + (size_t(q0) * p.heads + h) * D;
+  t.q_stride = size_t(p.heads) * D;
+  t.out = p.out + (size_t(q0) * p.heads + h) * D;
+  t.out_stride = size_t(p.heads) * D;
+  attn::attn_query_tile(t, qscale, sh);
 }
 
 }  // namespace
@@ -531,7 +421,7 @@ hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s) {
       p.pos0 + p.tokens > p.capacity || p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const float qscale = float(std::pow(128.0, -0.5)) * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(p.heads, (p.tokens + 127) / 128), dim3(256), 0, s,
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(p.heads, (p.tokens + 31) / 32), dim3(256), 0, s,
                      p, qscale);
   return hipGetLastError();
 }
