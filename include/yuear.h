@@ -278,7 +278,8 @@ int32_t yuear_op_qgemv(const uint32_t *dev_codes, const uint32_t *dev_groups, in
 int32_t yuear_op_dequantize(const uint32_t *dev_codes, const uint32_t *dev_groups,
                             int32_t bits, int32_t n, int32_t k, uint16_t *dev_out,
                             void *stream);
-/* C[m][n] = bf16(A[m] . W[n]) (+ C when residual) on MFMA. */
+/* C[m][n] = bf16(A[m] . W[n]), or C = bf16(C + bf16(A[m] . W[n])) when
+ * residual (the prefill projections, on hipBLASLt). */
 int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                       int32_t ldc, int32_t residual, void *stream);

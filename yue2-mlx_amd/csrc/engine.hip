@@ -1149,7 +1149,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       const LayerW &L = E.layers[l];
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.input_ln, c.eps, S.ph, st));
       GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0};
-      HIPC(launch_gemm(g, st));
+      HIPC(launch_gemm(g, nullptr, st));
       QkPrepParams qp;
       qp.qkv = S.pqkv;
       qp.qkv_stride = c.qkv();
@@ -1181,13 +1181,13 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       ap.out = S.pattn;
       HIPC(launch_attn_prefill(ap, st));
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
-      HIPC(launch_gemm(og, st));
+      HIPC(launch_gemm(og, S.ph, st));  // S.ph is free until the next RMSNorm
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
       GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pgu, 2 * c.F, 0};
-      HIPC(launch_gemm(gu, st));
+      HIPC(launch_gemm(gu, nullptr, st));
       HIPC(launch_swiglu_rows(S.pgu, T, c.F, S.pact, st));
       GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1};
-      HIPC(launch_gemm(dg, st));
+      HIPC(launch_gemm(dg, S.ph, st));
     }
     S.host_pos[b] += T;
     if (start + T >= n)  // final norm + projection of the last hidden row
@@ -2081,7 +2081,23 @@ int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
 int32_t yuear_op_gemm(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t m, int32_t n,
                       int32_t k, uint16_t *c, int32_t ldc, int32_t residual, void *stream) {
   GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
-  return int32_t(launch_gemm(p, static_cast<hipStream_t>(stream)));
+  if (!residual)
+    return int32_t(launch_gemm(p, nullptr, static_cast<hipStream_t>(stream)));
+  // the residual form needs a [m][ldc] scratch matrix: a small per-process
+  // pool, grown on demand (as the batched GEMV's staging rows)
+  static std::mutex mu;
+  static uint16_t *scratch = nullptr;
+  static size_t scratch_elems = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const size_t need = size_t(m) * ldc;
+  if (need > scratch_elems) {
+    if (scratch) (void)hipFree(scratch);
+    scratch = nullptr;
+    scratch_elems = 0;
+    if (hipMalloc(&scratch, need * 2) != hipSuccess) return int32_t(hipErrorOutOfMemory);
+    scratch_elems = need;
+  }
+  return int32_t(launch_gemm(p, scratch, static_cast<hipStream_t>(stream)));
 }
 
 int32_t yuear_op_attention_prefill(const uint16_t *q, const uint16_t *k_cache,

@@ -195,7 +195,10 @@ struct GemmParams {
   int ldc = 0;
   int residual = 0;             // c = bf16(c + bf16(acc))
 };
-hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
+// On hipBLASLt (blas.hip). The residual form needs `scratch`, a [m][ldc]
+// bf16 matrix that receives bf16(acc) before the add (n and ldc multiples
+// of 8).
+hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, hipStream_t s);
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
                              int width, uint16_t *out, hipStream_t s);

@@ -1,6 +1,6 @@
-// Prompt prefill kernels on gfx950: MFMA bf16 GEMM for the projections,
-// row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV append, and
-// an MFMA causal attention with fp32 opmath.
+// Prompt prefill kernels on gfx950 (the projections are GEMMs on hipBLASLt,
+// blas.hip): row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV
+// append, and an MFMA causal attention with fp32 opmath.
 //
 // Reference: native/src/ar.cpp:246-301 (hidden() over T > 1 tokens) and
 // native/src/sampling.cpp:152-183 (prefill). The reference upcasts Q/K/V to
@@ -18,226 +18,6 @@ namespace yuear {
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-// ---------------------------------------------------------------------------
-// GEMM: C[m][n] = sum_k A[m][k] W[n][k] (A tokens x hidden, W row-major
-// weights), fp32 accumulation on v_mfma_f32_32x32x16_bf16, bf16 output.
-// Block tile 128 x 128 x 64, four waves in a 2 x 2 arrangement of 64 x 64
-// wave tiles (2 x 2 MFMA tiles each). LDS holds one A and one W tile with
-// rows padded to 72 elements; the next K slab is prefetched into registers
-// while the current one feeds the MFMAs. Blocks are renumbered so that the
-// blocks sharing a weight tile land on the same XCD (shared L2).
-// ---------------------------------------------------------------------------
-constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;
-
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
-  __shared__ uint16_t As[BM * LDSW];
-  __shared__ uint16_t Bs[BN * LDSW];
-  const int tiles_m = (p.m + BM - 1) / BM;
-  const int nb = gridDim.x;
-  const int bid = blockIdx.x;
-  const int per = nb / 8, rem = nb % 8, xcd = bid % 8, slot = bid / 8;
-  const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  const int n_tile = logical / tiles_m, m_tile = logical % tiles_m;
-  const int m0 = m_tile * BM, n0 = n_tile * BN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // global -> register staging: 4 x 16 B of A and of W per thread
-  u32x4 ra[4], rb[4];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;
-      const int am = m0 + row, bn = n0 + row;
-      ra[c] = am < p.m ? *reinterpret_cast<const u32x4 *>(p.a + size_t(am) * p.lda + k0 + col)
-                       : u32x4{0u, 0u, 0u, 0u};
-      rb[c] = bn < p.n ? __builtin_nontemporal_load(
-                             reinterpret_cast<const u32x4 *>(p.w + size_t(bn) * p.k + k0 + col))
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&]() {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;
-      *reinterpret_cast<u32x4 *>(&As[row * LDSW + col]) = ra[c];
-      *reinterpret_cast<u32x4 *>(&Bs[row * LDSW + col]) = rb[c];
-    }
-  };
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[i][j][r] = 0.f;
-
-  load(0);
-  for (int k0 = 0; k0 < p.k; k0 += BK) {
-    __syncthreads();
-    store();
-    __syncthreads();
-    if (k0 + BK < p.k)
-      load(k0 + BK);
-#pragma unroll
-    for (int ks = 0; ks < BK; ks += 16) {
-      bf16x8_t af[2], bf[2];
-      const int kk = ks + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t *>(&As[(wm * 64 + i * 32 + (lane & 31)) * LDSW + kk]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const bf16x8_t *>(&Bs[(wn * 64 + j * 32 + (lane & 31)) * LDSW + kk]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // epilogue: lane holds column (lane % 32), rows 8(r/4) + 4(lane/32) + r%4
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (col >= p.n)
-        continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < p.m) {
-          uint16_t *dst = p.c + size_t(row) * p.ldc + col;
-          float v = acc[i][j][r];
-          if (p.residual)
-            v = bf2f(*dst) + rbf(v);
-          *dst = f2bf(v);
-        }
-      }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Large GEMM (prefill chunks with at least ~240 such tiles, e.g. QKV and
-// gate/up at 3000 tokens): block tile 256 x 256 x 64,
-// eight waves (two per SIMD) in a 2 x 4 arrangement of 128 x 64 wave tiles
-// (4 x 2 MFMA 32x32x16 tiles, 128 fp32 accumulators per lane), so each A
-// fragment read from LDS feeds two MFMAs and each W fragment four. LDS is
-// double-buffered (2 x (A + W) x 256 rows x 72 elements = 144 KiB of the
-// 160 KiB): the next K slab's global loads are in flight while the current
-// slab feeds the MFMAs, and one barrier per slab suffices.
-// ---------------------------------------------------------------------------
-constexpr int GM = 256, GN = 256, GK = 64, GP = GK + 8;
-constexpr size_t kGemm256Lds = size_t(2) * 2 * 256 * GP * sizeof(uint16_t);
-
-__global__ __launch_bounds__(512) void gemm256_kernel(GemmParams p) {
-  extern __shared__ uint16_t glds[];
-  const int tiles_m = (p.m + GM - 1) / GM;
-  const int nb = gridDim.x;
-  const int bid = blockIdx.x;
-  const int per = nb / 8, rem = nb % 8, xcd = bid % 8, slot = bid / 8;
-  const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  const int n_tile = logical / tiles_m, m_tile = logical % tiles_m;
-  const int m0 = m_tile * GM, n0 = n_tile * GN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;  // rows wm * 128, cols wn * 64
-  auto abuf = [&](int b) { return glds + size_t(b) * (2 * 256 * GP); };
-  auto bbuf = [&](int b) { return glds + size_t(b) * (2 * 256 * GP) + 256 * GP; };
-
-  // global -> register staging: 4 x 16 B of A and of W per thread
-  u32x4 ra[4], rb[4];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 512 * c, row = idx >> 3, col = (idx & 7) * 8;
-      const int am = m0 + row, bn = n0 + row;
-      ra[c] = am < p.m ? *reinterpret_cast<const u32x4 *>(p.a + size_t(am) * p.lda + k0 + col)
-                       : u32x4{0u, 0u, 0u, 0u};
-      rb[c] = bn < p.n ? __builtin_nontemporal_load(
-                             reinterpret_cast<const u32x4 *>(p.w + size_t(bn) * p.k + k0 + col))
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&](int b) {
-    uint16_t *As = abuf(b), *Bs = bbuf(b);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 512 * c, row = idx >> 3, col = (idx & 7) * 8;
-      *reinterpret_cast<u32x4 *>(&As[row * GP + col]) = ra[c];
-      *reinterpret_cast<u32x4 *>(&Bs[row * GP + col]) = rb[c];
-    }
-  };
-
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[i][j][r] = 0.f;
-
-  const int nk = p.k / GK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more)
-      load((kt + 1) * GK);
-    const uint16_t *As = abuf(cur), *Bs = bbuf(cur);
-#pragma unroll
-    for (int ks = 0; ks < GK; ks += 16) {
-      bf16x8_t af[4], bf[2];
-      const int kk = ks + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t *>(&As[(wm * 128 + i * 32 + (lane & 31)) * GP + kk]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const bf16x8_t *>(&Bs[(wn * 64 + j * 32 + (lane & 31)) * GP + kk]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (more)
-      store(cur ^ 1);
-    __syncthreads();
-  }
-
-  // epilogue: lane holds column (lane % 32), rows 8(r/4) + 4(lane/32) + r%4
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (col >= p.n)
-        continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < p.m) {
-          uint16_t *dst = p.c + size_t(row) * p.ldc + col;
-          float v = acc[i][j][r];
-          if (p.residual)
-            v = bf2f(*dst) + rbf(v);
-          *dst = f2bf(v);
-        }
-      }
-    }
-}
 
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_rows_kernel(const uint16_t *table, const int32_t *ids,
@@ -360,28 +140,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 }  // namespace
-
-hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
-  if (p.m < 1 || p.n < 1 || p.k % BK || p.lda % 8 || p.ldc < p.n)
-    return hipErrorInvalidValue;
-  const int big_blocks = ((p.m + GM - 1) / GM) * ((p.n + GN - 1) / GN);
-  if (big_blocks >= 240) {  // enough 256 x 256 tiles to fill the GPU (K % 64 == 0 here)
-    static bool lds_set = false;
-    if (!lds_set) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm256_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         int(kGemm256Lds));
-      if (e != hipSuccess)
-        return e;
-      lds_set = true;
-    }
-    hipLaunchKernelGGL(gemm256_kernel, dim3(big_blocks), dim3(512), kGemm256Lds, s, p);
-    return hipGetLastError();
-  }
-  const int blocks = ((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
-  hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(256), 0, s, p);
-  return hipGetLastError();
-}
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows, int width,
                              uint16_t *out, hipStream_t s) {
