@@ -218,6 +218,19 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
   const int end = p.phase == kPhaseAbc ? kEOD : p.phase == kPhaseSemantic ? 0 : -1;
   const bool end_masked = end >= 0 && end < n && step < p.min_tokens;  // sampling.cpp:47-50
 
+  // Greedy without CFG: this thread's logit chunks are loaded first, so
+  // their latency overlaps the special-row set-up below (kPre chunks per
+  // thread cover 90112 logits in one round).
+  constexpr int kPre = 11;
+  const int n8 = n >> 3;
+  const bool prefetch = greedy && !cx.cfg;
+  u32x4 pre[kPre];
+  if (prefetch) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u)
+      pre[u] = reinterpret_cast<const u32x4 *>(p.logits)[min(tid + u * kT, max(n8 - 1, 0))];
+  }
+
   // Special rows: the end row while masked and the distinct local ids of the
   // penalty window (sampling.cpp:51-75); everything else is a plain score.
   const int nw = (n + 31) >> 5;
@@ -257,12 +270,30 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
     return v;
   };
 
-  const int n8 = n >> 3;
   int local = 0;
   if (greedy) {  // sampling.cpp:247: argmax, lowest index on ties
     float bv = ninf;
     int bi = 0x7fffffff;
-    for (int c0 = tid; c0 < n8; c0 += 2 * kT) {
+    int c_from = tid;
+    if (prefetch) {
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int c = tid + u * kT;
+        if (c >= n8)
+          break;
+        const uint32_t w[4] = {pre[u].x, pre[u].y, pre[u].z, pre[u].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = e & 1 ? bfhi(w[e >> 1]) : bflo(w[e >> 1]);
+          if (!special(sh, 8 * c + e) && better(v, 8 * c + e, bv, bi)) {
+            bv = v;
+            bi = 8 * c + e;
+          }
+        }
+      }
+      c_from = tid + kPre * kT;
+    }
+    for (int c0 = c_from; c0 < n8; c0 += 2 * kT) {
       float v[2][8];
       const int c1 = min(c0 + kT, n8 - 1);
       cx.chunk(c0, v[0]);
