@@ -342,9 +342,15 @@ hipError_t launch_r(const GemvParams &p, hipStream_t s) {
 
 template <int B, int BITS, int L, int P>
 hipError_t launch_lp(const GemvParams &p, hipStream_t s) {
-  // two row sets per wave for the long GEMVs (lm_head, gate/up) when that
-  // still leaves >= 1024 workgroups; one otherwise (more workgroups for the
-  // short ones, whose time is latency)
+  // more row sets per wave for the long GEMVs (lm_head, gate/up) while that
+  // still leaves >= 1024 workgroups: each workgroup's activation staging is
+  // then shared by more rows (4-bit lm_head: 47.7 / 36.1 / 31.9 us with
+  // 1 / 2 / 4 sets); one set for the short ones, whose time is latency
+  if constexpr (P <= 3) {
+    constexpr int rows4 = 16 * (64 / L);
+    if ((p.n + rows4 - 1) / rows4 >= 1024)
+      return launch_r<B, BITS, L, P, 4>(p, s);
+  }
   if constexpr (P <= 4) {
     constexpr int rows2 = 8 * (64 / L);
     if ((p.n + rows2 - 1) / rows2 >= 1024)
