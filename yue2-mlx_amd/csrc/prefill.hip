@@ -68,46 +68,91 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const uint16_t *x, i
   }
 }
 
-// ar.cpp:36-51 on interleaved (gate_i, up_i) columns.
+// ar.cpp:36-51 on interleaved (gate_i, up_i) columns: 4 pairs (16 bytes in,
+// 8 bytes out) per thread and vector, 4 vectors loaded before the first is
+// used; f a multiple of 4.
 __global__ __launch_bounds__(256) void swiglu_rows_kernel(const uint16_t *gu, int f,
                                                           uint16_t *out) {
   const int r = blockIdx.x;
-  const uint32_t *src = reinterpret_cast<const uint32_t *>(gu + size_t(r) * 2 * f);
-  for (int i = threadIdx.x; i < f; i += 256) {
-    const uint32_t pair = src[i];
-    const float g = bflo(pair), u = bfhi(pair);
-    const float act = rbf(g * (1.0f / (1.0f + expf(-g))));
-    out[size_t(r) * f + i] = f2bf(act * u);
+  const u32x4 *src = reinterpret_cast<const u32x4 *>(gu + size_t(r) * 2 * f);
+  uint2 *dst = reinterpret_cast<uint2 *>(out + size_t(r) * f);
+  constexpr int kIn = 4;  // loads in flight per thread
+  const int nv = f / 4;
+  for (int i0 = threadIdx.x; i0 < nv; i0 += 256 * kIn) {
+    u32x4 v[kIn];
+#pragma unroll
+    for (int k = 0; k < kIn; ++k)
+      v[k] = src[min(i0 + 256 * k, nv - 1)];
+#pragma unroll
+    for (int k = 0; k < kIn; ++k) {
+      const int i = i0 + 256 * k;
+      if (i >= nv)
+        break;
+      const uint32_t pairs[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float g = bflo(pairs[j]), u = bfhi(pairs[j]);
+        const float act = rbf(g * (1.0f / (1.0f + expf(-g))));
+        o[j] = f2bf(act * u);
+      }
+      dst[i] = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    }
   }
 }
 
 // q/k RMSNorm + RoPE for T tokens, K/V append (ar.cpp:268-282).
-__global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
-  const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// One workgroup per token; wave w takes heads w, w + 4, ... and issues the
+// loads of up to 8 of them before the first reduction, so each wave keeps
+// several independent loads in flight (the per-head work is a short
+// dependent chain: load, cross-lane sum, rotate, store). Workgroup i runs on
+// XCD i mod 8: token t = (i mod 8) * per + i / 8 keeps runs of consecutive
+// tokens on one XCD, so the 2-byte V stores of neighbouring slots (one
+// 64-byte block column per dim) merge in that XCD's L2 before write-back.
+__global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p, int per) {
+  constexpr int kBatch = 8;
+  const int t = int(blockIdx.x % 8) * per + int(blockIdx.x / 8);
+  if (t >= p.tokens)
+    return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int pos = p.pos0 + t;
-  const uint16_t *row = p.qkv + size_t(t) * p.qkv_stride;
-  const uint16_t *cs = p.rope_cos + size_t(pos) * 64;
-  const uint16_t *sn = p.rope_sin + size_t(pos) * 64;
+  const uint32_t *row = reinterpret_cast<const uint32_t *>(p.qkv + size_t(t) * p.qkv_stride);
+  NormRope rq, rk;
+  load_rope(rq, p.rope_cos + size_t(pos) * 64, p.rope_sin + size_t(pos) * 64, lane);
+  rk = rq;
+  if (p.q_norm)
+    load_gain(rq, p.q_norm, lane);
+  if (p.k_norm)
+    load_gain(rk, p.k_norm, lane);
   const int nh = p.heads + 2 * p.kv_heads;
-  for (int h = wave + 4 * blockIdx.y; h < nh; h += 4 * gridDim.y) {
-    const uint32_t pair = reinterpret_cast<const uint32_t *>(row + size_t(h) * 128)[lane];
-    float y0 = bflo(pair), y1 = bfhi(pair);
-    uint32_t *dst;
-    if (h < p.heads) {
-      norm_rope_head(y0, y1, p.q_norm, p.eps, cs, sn, lane, y0, y1);
-      dst = reinterpret_cast<uint32_t *>(p.q_out + (size_t(t) * p.heads + h) * 128);
-    } else if (h < p.heads + p.kv_heads) {
-      const int kvh = h - p.heads;
-      norm_rope_head(y0, y1, p.k_norm, p.eps, cs, sn, lane, y0, y1);
-      dst = reinterpret_cast<uint32_t *>(p.k_cache + (size_t(kvh) * p.capacity + pos) * 128);
-    } else {  // V: dims 2 lane, 2 lane + 1 into the slot's 32-key block column
-      const int kvh = h - p.heads - p.kv_heads;
-      uint16_t *vh = p.v_cache + size_t(kvh) * p.capacity * 128;
-      vh[attn::v_index(pos, 2 * lane)] = f2bf(y0);
-      vh[attn::v_index(pos, 2 * lane + 1)] = f2bf(y1);
-      continue;
+  for (int h0 = wave; h0 < nh; h0 += 4 * kBatch) {
+    uint32_t pair[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      pair[j] = row[size_t(min(h0 + 4 * j, nh - 1)) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int h = h0 + 4 * j;  // uniform per wave
+      if (h >= nh)
+        break;
+      float y0 = bflo(pair[j]), y1 = bfhi(pair[j]);
+      uint32_t *dst;
+      if (h < p.heads) {
+        norm_rope_apply(y0, y1, p.q_norm != nullptr, p.eps, rq, lane, y0, y1);
+        dst = reinterpret_cast<uint32_t *>(p.q_out + (size_t(t) * p.heads + h) * 128);
+      } else if (h < p.heads + p.kv_heads) {
+        const int kvh = h - p.heads;
+        norm_rope_apply(y0, y1, p.k_norm != nullptr, p.eps, rk, lane, y0, y1);
+        dst = reinterpret_cast<uint32_t *>(p.k_cache + (size_t(kvh) * p.capacity + pos) * 128);
+      } else {  // V: dims 2 lane, 2 lane + 1 into the slot's 32-key block column
+        const int kvh = h - p.heads - p.kv_heads;
+        uint16_t *vh = p.v_cache + size_t(kvh) * p.capacity * 128;
+        vh[attn::v_index(pos, 2 * lane)] = f2bf(y0);
+        vh[attn::v_index(pos, 2 * lane + 1)] = f2bf(y1);
+        continue;
+      }
+      dst[lane] = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
     }
-    dst[lane] = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
   }
 }
 
@@ -158,7 +203,7 @@ hipError_t launch_rms_norm_rows(const uint16_t *x, int rows, int width, const ui
 }
 
 hipError_t launch_swiglu_rows(const uint16_t *gu, int rows, int f, uint16_t *out, hipStream_t s) {
-  if (rows < 1 || f < 1)
+  if (rows < 1 || f < 4 || f % 4)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(swiglu_rows_kernel, dim3(rows), dim3(256), 0, s, gu, f, out);
   return hipGetLastError();
@@ -168,9 +213,8 @@ hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
   if (p.head_dim != 128 || p.tokens < 1 || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity ||
       p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
-  const int nh = p.heads + 2 * p.kv_heads;
-  const int gy = (nh + 3) / 4;
-  hipLaunchKernelGGL(qk_prep_kernel, dim3(p.tokens, gy), dim3(256), 0, s, p);
+  const int per = (p.tokens + 7) / 8;
+  hipLaunchKernelGGL(qk_prep_kernel, dim3(8 * per), dim3(256), 0, s, p, per);
   return hipGetLastError();
 }
 
