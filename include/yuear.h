@@ -249,7 +249,12 @@ yuear_status yuear_session_time_kernel(yuear_session *session,
                                        double *ms_per_launch, char **error_json);
 
 /* ---- op-level entry points (model_ops, ar.hpp:8-19), device pointers,
- * `stream` is a hipStream_t (NULL = default stream) ---- */
+ * `stream` is a hipStream_t (NULL = default stream). Scratch memory (the
+ * batched GEMV's staging rows, the decode attention's split partials, the
+ * GEMM's residual matrix and library workspace) is per (device, stream):
+ * calls on different streams never share it. The first call on a stream (or
+ * one needing a larger buffer) allocates, so make it outside graph capture;
+ * yuear_op_gemm allocates stream-ordered (hipMallocAsync) on every call. ---- */
 /* y[b][r] = bf16(x[b] . W[row(r)]) with optional RMSNorm prologue
  * (norm_w != NULL) and epilogue 0 store / 1 residual add / 2 SwiGLU pairs. */
 int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,

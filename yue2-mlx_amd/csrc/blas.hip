@@ -9,8 +9,10 @@
 // product to a scratch matrix first and adds it in a second kernel, keeping
 // the reference's two rounding points.
 //
-// One library handle and workspace per device, created on first use; the
-// algorithm chosen by the library's heuristic is cached per shape.
+// One library handle per device, created on first use; the algorithm chosen
+// by the library's heuristic (allowed up to kGemmWorkspace bytes of
+// workspace) is cached per shape. The workspace belongs to the caller (one
+// per stream that runs GEMMs), so concurrent streams never share one.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -25,12 +27,14 @@ namespace yuear {
 
 namespace {
 
-constexpr size_t kWorkspace = size_t(64) << 20;
+struct Algo {
+  hipblasLtMatmulAlgo_t algo;
+  size_t workspace;  // bytes the algorithm needs
+};
 
 struct Lt {
   hipblasLtHandle_t handle = nullptr;
-  void *workspace = nullptr;
-  std::map<std::tuple<int, int, int, int, int>, hipblasLtMatmulAlgo_t> algos;
+  std::map<std::tuple<int, int, int, int, int>, Algo> algos;
 };
 
 std::mutex g_mu;
@@ -60,27 +64,20 @@ __global__ __launch_bounds__(256) void add_rows_kernel(uint16_t *x, const uint16
   *xp = u32x4{o[0], o[1], o[2], o[3]};
 }
 
-}  // namespace
-
-hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, hipStream_t s) {
-  if (p.m < 1 || p.n < 1 || p.k < 1 || p.lda < p.k || p.ldc < p.n || !p.a || !p.w || !p.c ||
-      (p.residual && (!scratch || p.n % 8 || p.ldc % 8)))
-    return hipErrorInvalidValue;
+// Validates p, creates the device's handle on first use and finds (or
+// caches) the algorithm for p's shape; desc / layouts are created for the
+// caller, who destroys them. Called with g_mu held.
+hipblasStatus_t prepare(const GemmParams &p, Lt *&lt, const Algo *&algo, hipblasLtMatmulDesc_t &desc,
+                        hipblasLtMatrixLayout_t &la, hipblasLtMatrixLayout_t &lb,
+                        hipblasLtMatrixLayout_t &lc) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess)
-    return e;
-  std::lock_guard<std::mutex> lock(g_mu);
-  Lt &lt = g_lt[dev];
-  if (!lt.handle) {
-    if (hipblasLtCreate(&lt.handle) != HIPBLAS_STATUS_SUCCESS)
-      return hipErrorUnknown;
-    e = hipMalloc(&lt.workspace, kWorkspace);
-    if (e != hipSuccess)
-      return e;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return HIPBLAS_STATUS_INTERNAL_ERROR;
+  lt = &g_lt[dev];
+  if (!lt->handle && hipblasLtCreate(&lt->handle) != HIPBLAS_STATUS_SUCCESS) {
+    lt->handle = nullptr;
+    return HIPBLAS_STATUS_NOT_INITIALIZED;
   }
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   hipblasStatus_t st = hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
   if (st == HIPBLAS_STATUS_SUCCESS)
@@ -93,36 +90,84 @@ hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, hipStream_t s) {
     st = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16BF, p.k, p.m, p.lda);
   if (st == HIPBLAS_STATUS_SUCCESS)
     st = hipblasLtMatrixLayoutCreate(&lc, HIP_R_16BF, p.n, p.m, p.ldc);
+  if (st != HIPBLAS_STATUS_SUCCESS)
+    return st;
   const auto key = std::make_tuple(p.m, p.n, p.k, p.lda, p.ldc);
-  auto it = lt.algos.find(key);
-  if (st == HIPBLAS_STATUS_SUCCESS && it == lt.algos.end()) {
+  auto it = lt->algos.find(key);
+  if (it == lt->algos.end()) {
     hipblasLtMatmulPreference_t pref = nullptr;
     st = hipblasLtMatmulPreferenceCreate(&pref);
-    const uint64_t ws = kWorkspace;
+    const uint64_t ws = kGemmWorkspace;
     if (st == HIPBLAS_STATUS_SUCCESS)
       st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES,
                                                  &ws, sizeof(ws));
     hipblasLtMatmulHeuristicResult_t result[1];
     int found = 0;
     if (st == HIPBLAS_STATUS_SUCCESS)
-      st = hipblasLtMatmulAlgoGetHeuristic(lt.handle, desc, la, lb, lc, lc, pref, 1, result, &found);
+      st = hipblasLtMatmulAlgoGetHeuristic(lt->handle, desc, la, lb, lc, lc, pref, 1, result, &found);
     if (pref)
       hipblasLtMatmulPreferenceDestroy(pref);
     if (st == HIPBLAS_STATUS_SUCCESS && found < 1)
       st = HIPBLAS_STATUS_NOT_SUPPORTED;
-    if (st == HIPBLAS_STATUS_SUCCESS)
-      it = lt.algos.emplace(key, result[0].algo).first;
+    if (st != HIPBLAS_STATUS_SUCCESS)
+      return st;
+    it = lt->algos.emplace(key, Algo{result[0].algo, result[0].workspaceSize}).first;
   }
-  if (st == HIPBLAS_STATUS_SUCCESS) {
-    const float alpha = 1.f, beta = 0.f;
-    uint16_t *d = p.residual ? scratch : p.c;
-    st = hipblasLtMatmul(lt.handle, desc, &alpha, p.w, la, p.a, lb, &beta, d, lc, d, lc,
-                         &it->second, lt.workspace, kWorkspace, s);
-  }
+  algo = &it->second;
+  return HIPBLAS_STATUS_SUCCESS;
+}
+
+void destroy(hipblasLtMatmulDesc_t desc, hipblasLtMatrixLayout_t la, hipblasLtMatrixLayout_t lb,
+             hipblasLtMatrixLayout_t lc) {
   if (lc) hipblasLtMatrixLayoutDestroy(lc);
   if (lb) hipblasLtMatrixLayoutDestroy(lb);
   if (la) hipblasLtMatrixLayoutDestroy(la);
   if (desc) hipblasLtMatmulDescDestroy(desc);
+}
+
+bool valid(const GemmParams &p) {
+  return p.m >= 1 && p.n >= 1 && p.k >= 1 && p.lda >= p.k && p.ldc >= p.n && p.a && p.w && p.c;
+}
+
+}  // namespace
+
+hipError_t gemm_workspace_bytes(const GemmParams &p, size_t *bytes) {
+  if (!valid(p) || !bytes)
+    return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lock(g_mu);
+  Lt *lt = nullptr;
+  const Algo *algo = nullptr;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  const hipblasStatus_t st = prepare(p, lt, algo, desc, la, lb, lc);
+  destroy(desc, la, lb, lc);
+  if (st != HIPBLAS_STATUS_SUCCESS)
+    return status_error(st);
+  *bytes = algo->workspace;
+  return hipSuccess;
+}
+
+hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, void *workspace,
+                       size_t workspace_bytes, hipStream_t s) {
+  if (!valid(p) || (p.residual && (!scratch || p.n % 8 || p.ldc % 8)))
+    return hipErrorInvalidValue;
+  std::lock_guard<std::mutex> lock(g_mu);
+  Lt *lt = nullptr;
+  const Algo *algo = nullptr;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasStatus_t st = prepare(p, lt, algo, desc, la, lb, lc);
+  if (st == HIPBLAS_STATUS_SUCCESS && algo->workspace > (workspace ? workspace_bytes : 0)) {
+    destroy(desc, la, lb, lc);
+    return hipErrorInvalidValue;  // the caller's workspace is too small
+  }
+  if (st == HIPBLAS_STATUS_SUCCESS) {
+    const float alpha = 1.f, beta = 0.f;
+    uint16_t *d = p.residual ? scratch : p.c;
+    st = hipblasLtMatmul(lt->handle, desc, &alpha, p.w, la, p.a, lb, &beta, d, lc, d, lc,
+                         &algo->algo, workspace, workspace ? workspace_bytes : 0, s);
+  }
+  destroy(desc, la, lb, lc);
   if (st != HIPBLAS_STATUS_SUCCESS)
     return status_error(st);
   if (p.residual) {

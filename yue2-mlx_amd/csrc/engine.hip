@@ -277,6 +277,7 @@ struct yuear_session {
   int scratch_u_stride = 0;
   // prefill scratch
   int chunk = 0;
+  void *gemm_ws = nullptr;  // prefill GEMM workspace (kGemmWorkspace bytes)
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
            *pgu = nullptr, *pact = nullptr;
   int32_t *pids = nullptr;
@@ -674,6 +675,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   const size_t T = S.chunk;
   S.px = S.alloc<uint16_t>(T * c.H);
   S.ph = S.alloc<uint16_t>(T * c.H);
+  S.gemm_ws = S.alloc<uint8_t>(kGemmWorkspace);  // hipBLASLt scratch of this session's stream
   S.pqkv = S.alloc<uint16_t>(T * c.qkv());
   S.pq = S.alloc<uint16_t>(T * c.Hq * c.D);
   S.pattn = S.alloc<uint16_t>(T * c.Hq * c.D);
@@ -1149,7 +1151,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       const LayerW &L = E.layers[l];
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.input_ln, c.eps, S.ph, st));
       GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0};
-      HIPC(launch_gemm(g, nullptr, st));
+      HIPC(launch_gemm(g, nullptr, S.gemm_ws, kGemmWorkspace, st));
       QkPrepParams qp;
       qp.qkv = S.pqkv;
       qp.qkv_stride = c.qkv();
@@ -1181,13 +1183,13 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       ap.out = S.pattn;
       HIPC(launch_attn_prefill(ap, st));
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
-      HIPC(launch_gemm(og, S.ph, st));  // S.ph is free until the next RMSNorm
+      HIPC(launch_gemm(og, S.ph, S.gemm_ws, kGemmWorkspace, st));  // S.ph is free until the next RMSNorm
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
       GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pgu, 2 * c.F, 0};
-      HIPC(launch_gemm(gu, nullptr, st));
+      HIPC(launch_gemm(gu, nullptr, S.gemm_ws, kGemmWorkspace, st));
       HIPC(launch_swiglu_rows(S.pgu, T, c.F, S.pact, st));
       GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1};
-      HIPC(launch_gemm(dg, S.ph, st));
+      HIPC(launch_gemm(dg, S.ph, S.gemm_ws, kGemmWorkspace, st));
     }
     S.host_pos[b] += T;
     if (start + T >= n)  // final norm + projection of the last hidden row
@@ -1288,6 +1290,40 @@ void check_sampler_phase(yuear_session &S, double cfg_scale) {
 
 // ===========================================================================
 // C ABI
+namespace {
+// Scratch of the op-level entry points, one buffer per (device, stream):
+// calls on one stream are ordered and may share it, calls on different
+// streams or devices never do. Grown on demand (the stream is synchronised
+// before the smaller buffer is freed), kept until the process ends.
+struct OpPool {
+  std::mutex mu;
+  std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> bufs;
+  hipError_t get(hipStream_t s, size_t bytes, void **out, bool *fresh) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+      return e;
+    std::lock_guard<std::mutex> lock(mu);
+    auto &b = bufs[{dev, s}];
+    *fresh = false;
+    if (bytes > b.second) {
+      if (b.first) {
+        if ((e = hipStreamSynchronize(s)) != hipSuccess)
+          return e;
+        (void)hipFree(b.first);
+      }
+      b = {nullptr, 0};
+      if ((e = hipMalloc(&b.first, bytes)) != hipSuccess)
+        return e;
+      b.second = bytes;
+      *fresh = true;
+    }
+    *out = b.first;
+    return hipSuccess;
+  }
+};
+}  // namespace
+
 extern "C" {
 
 const char *yuear_build_identifier(void) {
@@ -1892,21 +1928,15 @@ int32_t yuear_op_gemv(const uint16_t *w, int32_t n, int32_t k, int32_t batch, co
   p.y_stride = y_stride;
   p.epilogue = epilogue;
   if (batch >= 3 && norm_w && k > 0) {
-    // the batched form normalises the rows once into a scratch buffer,
-    // owned by a small per-process pool like the attention partials
-    static std::mutex mu;
-    static uint16_t *stage = nullptr;
-    static size_t stage_elems = 0;
-    std::lock_guard<std::mutex> lock(mu);
-    const size_t need = size_t(batch) * k;
-    if (need > stage_elems) {
-      if (stage) (void)hipFree(stage);
-      stage = nullptr;
-      stage_elems = 0;
-      if (hipMalloc(&stage, need * 2) != hipSuccess) return int32_t(hipErrorOutOfMemory);
-      stage_elems = need;
-    }
-    p.stage = stage;
+    // the batched form normalises the rows once into a scratch buffer
+    static OpPool pool;
+    void *stage = nullptr;
+    bool fresh = false;
+    const hipError_t e = pool.get(static_cast<hipStream_t>(stream), size_t(batch) * k * 2, &stage,
+                                  &fresh);
+    if (e != hipSuccess)
+      return int32_t(e);
+    p.stage = static_cast<uint16_t *>(stage);
     return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
   }
   return int32_t(launch_gemv(p, static_cast<hipStream_t>(stream)));
@@ -2032,27 +2062,24 @@ int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
                                   const int32_t *pos, int32_t heads, int32_t kv_heads,
                                   int32_t capacity, int32_t batch, int32_t max_splits,
                                   uint16_t *out, void *stream) {
-  // partial buffers and counters owned by a small per-process pool
-  static std::mutex mu;
-  static float *part = nullptr;
-  static int32_t *counters = nullptr;
-  static size_t part_floats = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  const int G = kv_heads > 0 ? heads / kv_heads : 1;
-  const size_t need = size_t(batch) * kv_heads * max_splits * G * (128 + 2);
-  if (need > part_floats) {
-    if (part) (void)hipFree(part);
-    if (counters) (void)hipFree(counters);
-    part = nullptr;
-    counters = nullptr;
-    part_floats = 0;
-    if (hipMalloc(&part, need * 4) != hipSuccess) return int32_t(hipErrorOutOfMemory);
-    if (hipMalloc(&counters, 64 * 8 * 4) != hipSuccess) return int32_t(hipErrorOutOfMemory);
-    if (hipMemset(counters, 0, 64 * 8 * 4) != hipSuccess) return int32_t(hipErrorUnknown);
-    part_floats = need;
-  }
-  if (size_t(batch) * kv_heads > 64 * 8)
+  // split partials and arrival counters (zero between launches: the merging
+  // workgroup resets its counter) from a per-(device, stream) pool
+  if (batch < 1 || kv_heads < 1 || max_splits < 1 || size_t(batch) * kv_heads > 64 * 8)
     return int32_t(hipErrorInvalidValue);
+  const int G = heads / kv_heads;
+  const size_t need = size_t(batch) * kv_heads * max_splits * std::max(G, 1) * (128 + 2);
+  static OpPool pool;
+  void *buf = nullptr;
+  bool fresh = false;
+  const size_t counter_bytes = 64 * 8 * 4;
+  hipError_t e = pool.get(static_cast<hipStream_t>(stream), counter_bytes + need * 4, &buf, &fresh);
+  if (e != hipSuccess)
+    return int32_t(e);
+  int32_t *counters = static_cast<int32_t *>(buf);
+  float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(buf) + counter_bytes);
+  if (fresh && (e = hipMemsetAsync(counters, 0, counter_bytes, static_cast<hipStream_t>(stream))) !=
+                   hipSuccess)
+    return int32_t(e);
   AttnDecodeParams p;
   p.qkv = qkv;
   p.qkv_stride = (heads + 2 * kv_heads) * 128;
@@ -2081,23 +2108,27 @@ int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
 int32_t yuear_op_gemm(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t m, int32_t n,
                       int32_t k, uint16_t *c, int32_t ldc, int32_t residual, void *stream) {
   GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
-  if (!residual)
-    return int32_t(launch_gemm(p, nullptr, static_cast<hipStream_t>(stream)));
-  // the residual form needs a [m][ldc] scratch matrix: a small per-process
-  // pool, grown on demand (as the batched GEMV's staging rows)
-  static std::mutex mu;
-  static uint16_t *scratch = nullptr;
-  static size_t scratch_elems = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  const size_t need = size_t(m) * ldc;
-  if (need > scratch_elems) {
-    if (scratch) (void)hipFree(scratch);
-    scratch = nullptr;
-    scratch_elems = 0;
-    if (hipMalloc(&scratch, need * 2) != hipSuccess) return int32_t(hipErrorOutOfMemory);
-    scratch_elems = need;
+  // stream-ordered scratch (the residual matrix, the library's workspace):
+  // calls on different streams or devices never share one
+  if (m < 1 || n < 1 || k < 1 || lda < k || ldc < n || !a || !w || !c)
+    return int32_t(hipErrorInvalidValue);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  size_t ws_bytes = 0;
+  hipError_t e = gemm_workspace_bytes(p, &ws_bytes);
+  if (e != hipSuccess)
+    return int32_t(e);
+  const size_t res_bytes = residual ? size_t(m) * ldc * 2 : 0;
+  uint8_t *buf = nullptr;
+  if (ws_bytes + res_bytes > 0) {
+    e = hipMallocAsync(reinterpret_cast<void **>(&buf), ws_bytes + res_bytes + 256, st);
+    if (e != hipSuccess)
+      return int32_t(e);
   }
-  return int32_t(launch_gemm(p, scratch, static_cast<hipStream_t>(stream)));
+  uint16_t *scratch = residual ? reinterpret_cast<uint16_t *>(buf) : nullptr;
+  void *ws = ws_bytes ? buf + (res_bytes + 255) / 256 * 256 : nullptr;
+  e = launch_gemm(p, scratch, ws, ws_bytes, st);
+  const hipError_t f = buf ? hipFreeAsync(buf, st) : hipSuccess;
+  return int32_t(e != hipSuccess ? e : f);
 }
 
 int32_t yuear_op_attention_prefill(const uint16_t *q, const uint16_t *k_cache,

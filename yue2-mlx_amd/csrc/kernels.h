@@ -197,8 +197,13 @@ struct GemmParams {
 };
 // On hipBLASLt (blas.hip). The residual form needs `scratch`, a [m][ldc]
 // bf16 matrix that receives bf16(acc) before the add (n and ldc multiples
-// of 8).
-hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, hipStream_t s);
+// of 8). `workspace` (workspace_bytes, at most kGemmWorkspace are used) is
+// the library's scratch for this stream: never shared with a GEMM in flight
+// on another stream. gemm_workspace_bytes gives what p's algorithm needs.
+constexpr size_t kGemmWorkspace = size_t(64) << 20;
+hipError_t gemm_workspace_bytes(const GemmParams &p, size_t *bytes);
+hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, void *workspace,
+                       size_t workspace_bytes, hipStream_t s);
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
                              int width, uint16_t *out, hipStream_t s);
