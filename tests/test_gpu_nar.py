@@ -41,6 +41,9 @@ def host(torch, t):
     (1, 4, 4, 40, 1, False),       # one key
     (1, 16, 8, 257, 257, True),    # causal conditioning prefill
     (2, 6, 3, 64, 64, True),
+    # >= 768 workgroups of 64 queries: the LDS-shared 64-query tile (ragged last tiles)
+    (2, 24, 8, 1000, 1100, False),
+    (1, 24, 8, 2050, 2050, True),
 ])
 def test_nar_attention_matches_oracle(torch, yuear_lib, oracle, B, Hq, Hkv, Lq, Lk, causal):
     print(f"[nar] B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} causal={causal}", flush=True)

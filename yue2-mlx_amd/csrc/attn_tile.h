@@ -187,5 +187,154 @@ __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale
   }
 }
 
+// ---------------------------------------------------------------------------
+// 64-query tile with K/V shared through LDS: wave w owns queries 16 w + i and
+// all four waves walk the same 32-key blocks. Each block's K and V are
+// fetched once per workgroup (each wave loads a quarter: K pieces and V dim
+// tiles 2 w, 2 w + 1 in the MFMA operand layout of load_k / load_v) into a
+// three-stage LDS ring, two blocks ahead of the one being computed; every
+// wave then reads its operands from LDS. Same arithmetic per query as
+// attn_query_tile (fp32 scores, exp2 online softmax, P as three truncated
+// bf16 pieces, fp32 sums, bf16(o / l)), with no merge across waves.
+// Workgroups of the 64-query tile below which the 32-query key-split tile
+// is faster: three per CU on MI355X's 256 CUs (measured: 384 workgroups of
+// 64 queries lose to 768 of 32, 768 of 64 win).
+constexpr int kTile64MinGroups = 768;
+
+struct Tile64Lds {
+  u32x4 k[3][8][64];  // [stage][piece][lane]
+  u32x4 v[3][8][64];
+};
+
+__device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qscale,
+                                                  Tile64Lds &sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane >> 4, i = lane & 15;
+  const int nblk = (t.kend + kBlock - 1) / kBlock;
+  const int last = t.kend - 1;
+  u32x4 qb[4];
+  {
+    const int qi = min(16 * wave + i, t.nq - 1);
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(t.q + size_t(qi) * t.q_stride);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qb[s] = src[4 * s + r];
+  }
+  const int kmax = t.causal_pos >= 0 ? t.causal_pos + 16 * wave + i : t.kv_len - 1;
+  // this wave's quarter of the block at kb: K pieces 2 w, 2 w + 1 (T = w / 2,
+  // s = 2 (w % 2) + {0, 1}) and V dim tiles 2 w, 2 w + 1, for target lane
+  auto fetch = [&](int kb, u32x4(&st)[4]) {
+    const int key = min(kb + key_ofs(wave >> 1, i), last);
+    const int s0 = 2 * (wave & 1);
+    st[0] = t.kc[size_t(key) * (D / 8) + 4 * s0 + r];
+    st[1] = t.kc[size_t(key) * (D / 8) + 4 * (s0 + 1) + r];
+    const u32x4 *base = t.vc + size_t(min(kb >> 5, last >> 5)) * (kBlock * D / 8);
+    st[2] = base[(32 * wave + i) * (kBlock / 8) + r];
+    st[3] = base[(32 * wave + 16 + i) * (kBlock / 8) + r];
+  };
+  auto stash = [&](int stage, const u32x4(&st)[4]) {
+    sh.k[stage][2 * wave][lane] = st[0];
+    sh.k[stage][2 * wave + 1][lane] = st[1];
+    sh.v[stage][2 * wave][lane] = st[2];
+    sh.v[stage][2 * wave + 1][lane] = st[3];
+  };
+
+  float m_run = -__builtin_inff(), l_run = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 nxt[4], nxt2[4];
+  fetch(0, nxt);
+  stash(0, nxt);
+  if (1 < nblk)
+    fetch(kBlock, nxt);
+  __syncthreads();
+  for (int b = 0; b < nblk; ++b) {
+    const int stage = b % 3, kb = b * kBlock;
+    if (b + 2 < nblk)  // uniform
+      fetch(kb + 2 * kBlock, nxt2);
+    u32x4 kr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      kr[j] = sh.k[stage][j][lane];
+    f32x4 st[2];
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      st[T] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        st[T] = mfma(kr[4 * T + s], qb[s], st[T]);
+    }
+    // lane (query 16 w + i, r): keys kb + 8 r + 4 T + u
+    float sc[8];
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        sc[4 * T + u] = kb + 8 * r + 4 * T + u <= kmax ? st[T][u] * qscale : -__builtin_inff();
+    float mx = sc[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e)
+      mx = fmaxf(mx, sc[e]);
+    mx = max_halves(max_row_pairs(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+    float ps = 0.f;
+    uint32_t pw[3][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float p0 = __builtin_amdgcn_exp2f(sc[2 * q] - m_use);
+      float p1 = __builtin_amdgcn_exp2f(sc[2 * q + 1] - m_use);
+      ps += p0;
+      ps += p1;
+      // three truncated bf16 pieces: the top 8, next 8 and last 8
+      // significant bits of p; each remainder is exact, so p is their sum
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const uint32_t u0 = __builtin_bit_cast(uint32_t, p0);
+        const uint32_t u1 = __builtin_bit_cast(uint32_t, p1);
+        pw[k][q] = (u0 >> 16) | (u1 & 0xffff0000u);
+        p0 -= __builtin_bit_cast(float, u0 & 0xffff0000u);
+        p1 -= __builtin_bit_cast(float, u1 & 0xffff0000u);
+      }
+    }
+    l_run = l_run * corr + ps;
+    m_run = m_new;
+    u32x4 vr[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      vr[dt] = sh.v[stage][dt][lane];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      o[dt] *= corr;
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        o[dt] = mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[dt]);
+    }
+    if (b + 1 < nblk)  // block b + 1 (loaded one step earlier) into its stage
+      stash((b + 1) % 3, nxt);
+    __syncthreads();
+    if (b + 2 < nblk) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        nxt[j] = nxt2[j];
+    }
+  }
+  // lane (query 16 w + i, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
+  const float L = sum_halves(sum_row_pairs(l_run));
+  const int qi = 16 * wave + i;
+  if (qi < t.nq) {
+    uint16_t *dst = t.out + size_t(qi) * t.out_stride;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint32_t lo = uint32_t(f2bf(o[dt][0] / L)) | (uint32_t(f2bf(o[dt][1] / L)) << 16);
+      const uint32_t hi = uint32_t(f2bf(o[dt][2] / L)) | (uint32_t(f2bf(o[dt][3] / L)) << 16);
+      *reinterpret_cast<uint2 *>(dst + 16 * dt + 4 * r) = uint2{lo, hi};
+    }
+  }
+}
+
 }  // namespace attn
 }  // namespace yuear

@@ -17,6 +17,7 @@
 // layout of the KV cache, in a caller-provided workspace; keys past Lk in the
 // last block are zero there (and masked in the scores).
 #include <cmath>
+#include <type_traits>
 
 #include "attn_core.h"
 #include "attn_tile.h"
@@ -58,18 +59,23 @@ __global__ __launch_bounds__(256) void nar_v_blocks_kernel(const uint16_t *v, in
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void nar_attn_kernel(NarAttnParams p, float qscale) {
-  __shared__ attn::TileLds sh;
+// T64: the 64-query tile with K/V shared through LDS (attn_query_tile64),
+// chosen when it yields enough workgroups to fill the GPU; otherwise the
+// 32-query tile whose four waves split the keys.
+template <bool T64>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? 3 : 2, T64 ? 3 : 2))) void nar_attn_kernel(NarAttnParams p, float qscale) {
+  constexpr int kQ = T64 ? 64 : 32;  // queries per workgroup
+  __shared__ std::conditional_t<T64, attn::Tile64Lds, attn::TileLds> sh;
   const int bh = blockIdx.x;  // batch * heads + head
   const int h = bh % p.heads, b = bh / p.heads;
   const int tile = p.causal ? gridDim.y - 1 - blockIdx.y : blockIdx.y;  // causal: longest first
-  const int q0 = tile * 32;
+  const int q0 = tile * kQ;
   const int kvh = h / (p.heads / p.kv_heads);
   const size_t kvhead = size_t(b) * p.kv_heads + kvh;
   attn::QueryTile t;
   t.kc = reinterpret_cast<const u32x4 *>(p.k) + kvhead * p.kv_len * (D / 8);
   t.vc = reinterpret_cast<const u32x4 *>(p.vb) + kvhead * p.kv_pad * (D / 8);
-  t.nq = min(32, p.q_len - q0);
+  t.nq = min(kQ, p.q_len - q0);
   t.kv_len = p.kv_len;
   t.kend = p.causal ? q0 + t.nq : p.kv_len;
   t.causal_pos = p.causal ? q0 : -1;
@@ -77,7 +83,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   t.q_stride = D;
   t.out = p.out + (size_t(bh) * p.q_len + q0) * D;
   t.out_stride = D;
-  attn::attn_query_tile(t, qscale, sh);
+  if constexpr (T64)
+    attn::attn_query_tile64(t, qscale, sh);
+  else
+    attn::attn_query_tile(t, qscale, sh);
 }
 
 // Inverse of nar_v_blocks_kernel for a cache head: keys [0, n) of each head
@@ -129,8 +138,12 @@ hipError_t launch_nar_attention(NarAttnParams p, hipStream_t s) {
     return e;
   // scale * log2(e) as in the reference kernel (nar_attention.cpp:95)
   const float qscale = 0.08838834764831845f * 1.4426950408889634f;
-  hipLaunchKernelGGL(nar_attn_kernel, dim3(p.batch * p.heads, (p.q_len + 31) / 32), dim3(256), 0,
-                     s, p, qscale);
+  if (p.batch * p.heads * ((p.q_len + 63) / 64) >= attn::kTile64MinGroups)
+    hipLaunchKernelGGL(nar_attn_kernel<true>, dim3(p.batch * p.heads, (p.q_len + 63) / 64),
+                       dim3(256), 0, s, p, qscale);
+  else
+    hipLaunchKernelGGL(nar_attn_kernel<false>, dim3(p.batch * p.heads, (p.q_len + 31) / 32),
+                       dim3(256), 0, s, p, qscale);
   return hipGetLastError();
 }
 

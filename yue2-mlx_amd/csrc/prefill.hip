@@ -8,6 +8,7 @@
 // exact products on MFMA, keeps scores, softmax and all sums in fp32 and
 // rounds only the output to bf16.
 #include <cmath>
+#include <type_traits>
 
 #include "attn_core.h"
 #include "attn_tile.h"
@@ -164,24 +165,32 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p, int per) {
 // longest causal range first, and all heads of a tile run together so the
 // K/V blocks are shared in L2.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
-  __shared__ attn::TileLds sh;
+// T64: the 64-query tile with K/V shared through LDS (attn_query_tile64),
+// chosen when it yields enough workgroups to fill the GPU; otherwise the
+// 32-query tile whose four waves split the keys.
+template <bool T64>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? 3 : 2, T64 ? 3 : 2))) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
+  constexpr int kQ = T64 ? 64 : 32;  // queries per workgroup
+  __shared__ std::conditional_t<T64, attn::Tile64Lds, attn::TileLds> sh;
   using attn::D;
   const int h = blockIdx.x;
   const int tile = gridDim.y - 1 - blockIdx.y;  // longest causal range first
-  const int q0 = tile * 32;
+  const int q0 = tile * kQ;
   const int kvh = h / (p.heads / p.kv_heads);
   attn::QueryTile t;
   t.kc = reinterpret_cast<const u32x4 *>(p.k_cache) + size_t(kvh) * p.capacity * (D / 8);
   t.vc = reinterpret_cast<const u32x4 *>(p.v_cache) + size_t(kvh) * p.capacity * (D / 8);
-  t.nq = min(32, p.tokens - q0);
+  t.nq = min(kQ, p.tokens - q0);
   t.kend = p.pos0 + q0 + t.nq;
   t.causal_pos = p.pos0 + q0;
   t.q = p.q + (size_t(q0) * p.heads + h) * D;
   t.q_stride = size_t(p.heads) * D;
   t.out = p.out + (size_t(q0) * p.heads + h) * D;
   t.out_stride = size_t(p.heads) * D;
-  attn::attn_query_tile(t, qscale, sh);
+  if constexpr (T64)
+    attn::attn_query_tile64(t, qscale, sh);
+  else
+    attn::attn_query_tile(t, qscale, sh);
 }
 
 }  // namespace
@@ -223,8 +232,12 @@ hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s) {
       p.pos0 + p.tokens > p.capacity || p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const float qscale = float(std::pow(128.0, -0.5)) * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_prefill_kernel, dim3(p.heads, (p.tokens + 31) / 32), dim3(256), 0, s,
-                     p, qscale);
+  if (p.heads * ((p.tokens + 63) / 64) >= attn::kTile64MinGroups)
+    hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3(p.heads, (p.tokens + 63) / 64), dim3(256),
+                       0, s, p, qscale);
+  else
+    hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3(p.heads, (p.tokens + 31) / 32), dim3(256),
+                       0, s, p, qscale);
   return hipGetLastError();
 }
 
