@@ -191,19 +191,27 @@ __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale
 // 64-query tile with K/V shared through LDS: wave w owns queries 16 w + i and
 // all four waves walk the same 32-key blocks. Each block's K and V are
 // fetched once per workgroup (each wave loads a quarter: K pieces and V dim
-// tiles 2 w, 2 w + 1 in the MFMA operand layout of load_k / load_v) into a
-// three-stage LDS ring, two blocks ahead of the one being computed; every
-// wave then reads its operands from LDS. Same arithmetic per query as
+// tiles 2 w, 2 w + 1 in the MFMA operand layout of load_k / load_v) into an
+// LDS ring ahead of the block being computed; every wave then reads its
+// operands from LDS. Same arithmetic per query as
 // attn_query_tile (fp32 scores, exp2 online softmax, P as three truncated
 // bf16 pieces, fp32 sums, bf16(o / l)), with no merge across waves.
 // Workgroups of the 64-query tile below which the 32-query key-split tile
-// is faster: three per CU on MI355X's 256 CUs (measured: 384 workgroups of
-// 64 queries lose to 768 of 32, 768 of 64 win).
+// is faster on MI355X's 256 CUs (measured: 384 workgroups of 64 queries lose
+// to 768 of 32; 768 of 64 tie, 1128 and 1536 of 64 win).
 constexpr int kTile64MinGroups = 768;
 
+#ifndef YUEAR_TILE64_STAGES
+#define YUEAR_TILE64_STAGES 2
+#endif
+// LDS ring depth (prefetch distance + 1). Two stages (32 KiB, 112 VGPRs, four
+// waves per SIMD) measured 2-4% faster than three (48 KiB, 131 VGPRs, three).
+constexpr int kTile64Stages = YUEAR_TILE64_STAGES;
+constexpr int kTile64Waves = kTile64Stages == 3 ? 3 : 4;  // waves per SIMD (LDS, registers)
+
 struct Tile64Lds {
-  u32x4 k[3][8][64];  // [stage][piece][lane]
-  u32x4 v[3][8][64];
+  u32x4 k[kTile64Stages][8][64];  // [stage][piece][lane]
+  u32x4 v[kTile64Stages][8][64];
 };
 
 __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qscale,
@@ -244,16 +252,22 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
     o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int S = kTile64Stages;
   u32x4 nxt[4], nxt2[4];
   fetch(0, nxt);
   stash(0, nxt);
-  if (1 < nblk)
+  if (S == 3 && 1 < nblk)
     fetch(kBlock, nxt);
   __syncthreads();
   for (int b = 0; b < nblk; ++b) {
-    const int stage = b % 3, kb = b * kBlock;
-    if (b + 2 < nblk)  // uniform
-      fetch(kb + 2 * kBlock, nxt2);
+    const int stage = b % S, kb = b * kBlock;
+    if constexpr (S == 3) {
+      if (b + 2 < nblk)  // uniform
+        fetch(kb + 2 * kBlock, nxt2);
+    } else {
+      if (b + 1 < nblk)
+        fetch(kb + kBlock, nxt);
+    }
     u32x4 kr[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -313,10 +327,10 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
       for (int k = 0; k < 3; ++k)
         o[dt] = mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[dt]);
     }
-    if (b + 1 < nblk)  // block b + 1 (loaded one step earlier) into its stage
-      stash((b + 1) % 3, nxt);
+    if (b + 1 < nblk)  // block b + 1 into its stage
+      stash((b + 1) % S, nxt);
     __syncthreads();
-    if (b + 2 < nblk) {
+    if (S == 3 && b + 2 < nblk) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         nxt[j] = nxt2[j];

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void nar_v_blocks_kernel(const uint16_t *v, in
 // chosen when it yields enough workgroups to fill the GPU; otherwise the
 // 32-query tile whose four waves split the keys.
 template <bool T64>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? 3 : 2, T64 ? 3 : 2))) void nar_attn_kernel(NarAttnParams p, float qscale) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? attn::kTile64Waves : 2, T64 ? attn::kTile64Waves : 2))) void nar_attn_kernel(NarAttnParams p, float qscale) {
   constexpr int kQ = T64 ? 64 : 32;  // queries per workgroup
   __shared__ std::conditional_t<T64, attn::Tile64Lds, attn::TileLds> sh;
   const int bh = blockIdx.x;  // batch * heads + head

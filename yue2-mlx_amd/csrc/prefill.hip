@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p, int per) {
 // chosen when it yields enough workgroups to fill the GPU; otherwise the
 // 32-query tile whose four waves split the keys.
 template <bool T64>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? 3 : 2, T64 ? 3 : 2))) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? attn::kTile64Waves : 2, T64 ? attn::kTile64Waves : 2))) void attn_prefill_kernel(AttnPrefillParams p, float qscale) {
   constexpr int kQ = T64 ? 64 : 32;  // queries per workgroup
   __shared__ std::conditional_t<T64, attn::Tile64Lds, attn::TileLds> sh;
   using attn::D;
