@@ -44,6 +44,8 @@ def host(torch, t):
     # >= 768 workgroups of 64 queries: the LDS-shared 64-query tile (ragged last tiles)
     (2, 24, 8, 1000, 1100, False),
     (1, 24, 8, 2050, 2050, True),
+    (32, 24, 8, 64, 1, False),     # 768 workgroups of 64 queries over one key
+    (16, 24, 8, 130, 130, True),   # 1152 workgroups, causal, 2-query last tiles
 ])
 def test_nar_attention_matches_oracle(torch, yuear_lib, oracle, B, Hq, Hkv, Lq, Lk, causal):
     print(f"[nar] B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} causal={causal}", flush=True)
