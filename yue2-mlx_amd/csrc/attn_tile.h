@@ -41,6 +41,12 @@ struct QueryTile {
   int nq = 0;                   // valid queries (1..32)
   uint16_t *out = nullptr;      // output row of query 0
   size_t out_stride = 0;
+  // attn_query_tile64 only: key blocks [blk0, blk1) of the tile (blk1 0: all)
+  // and, when set, an unnormalised partial per query instead of out: 132
+  // floats {o[128], m, l, pad} at part + query * 132 (m the running maximum in
+  // the exp2 domain, l the sum of exp2(s - m), o the sum of exp2(s - m) v)
+  int blk0 = 0, blk1 = 0;
+  float *part = nullptr;
 };
 
 __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale, TileLds &sh) {
@@ -218,7 +224,8 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
                                                   Tile64Lds &sh) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane >> 4, i = lane & 15;
-  const int nblk = (t.kend + kBlock - 1) / kBlock;
+  const int b_lo = t.blk0;
+  const int nblk = t.blk1 ? t.blk1 : (t.kend + kBlock - 1) / kBlock;  // blocks [b_lo, nblk)
   const int last = t.kend - 1;
   u32x4 qb[4];
   {
@@ -254,12 +261,12 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
     o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   constexpr int S = kTile64Stages;
   u32x4 nxt[4], nxt2[4];
-  fetch(0, nxt);
-  stash(0, nxt);
-  if (S == 3 && 1 < nblk)
-    fetch(kBlock, nxt);
+  fetch(b_lo * kBlock, nxt);
+  stash(b_lo % S, nxt);
+  if (S == 3 && b_lo + 1 < nblk)
+    fetch((b_lo + 1) * kBlock, nxt);
   __syncthreads();
-  for (int b = 0; b < nblk; ++b) {
+  for (int b = b_lo; b < nblk; ++b) {
     const int stage = b % S, kb = b * kBlock;
     if constexpr (S == 3) {
       if (b + 2 < nblk)  // uniform
@@ -339,6 +346,19 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
   // lane (query 16 w + i, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
   const float L = sum_halves(sum_row_pairs(l_run));
   const int qi = 16 * wave + i;
+  if (t.part) {
+    if (qi < t.nq) {
+      float *pq = t.part + size_t(qi) * 132;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<f32x4 *>(pq + 16 * dt + 4 * r) = o[dt];
+      if (r == 0) {
+        pq[128] = m_run;
+        pq[129] = L;
+      }
+    }
+    return;
+  }
   if (qi < t.nq) {
     uint16_t *dst = t.out + size_t(qi) * t.out_stride;
 #pragma unroll

@@ -2045,6 +2045,17 @@ yuear_status yuear_nar_attention(const uint16_t *q, const uint16_t *k, const uin
     p.k = k;
     p.v = v;
     p.vb = static_cast<uint16_t *>(workspace);
+    // split-key partials for launches too small to fill the GPU, from a
+    // per-(device, stream) pool
+    const size_t pf = nar_attention_part_floats(batch, heads, q_len, kv_len, causal != 0);
+    if (pf) {
+      static OpPool pool;
+      void *buf = nullptr;
+      bool fresh = false;
+      HIPC(pool.get(static_cast<hipStream_t>(stream), pf * 4, &buf, &fresh));
+      p.part = static_cast<float *>(buf);
+      p.part_floats = pf;
+    }
     p.out = out;
     p.batch = batch;
     p.heads = heads;

@@ -144,7 +144,15 @@ struct NarAttnParams {
   uint16_t *out = nullptr;
   int batch = 1, heads = 0, kv_heads = 0, q_len = 0, kv_len = 0, causal = 0;
   int kv_pad = 0;  // set by launch_nar_attention: kv_len rounded up to 32
+  // optional split-key scratch (nar_attention_part_floats() floats): with it,
+  // launches too small to fill the GPU split the keys over workgroups
+  float *part = nullptr;
+  size_t part_floats = 0;
+  int splits = 1;  // set by launch_nar_attention
 };
+// Floats of split-key partials that let launch_nar_attention split this
+// launch's keys (0: it never splits this shape).
+size_t nar_attention_part_floats(int batch, int heads, int q_len, int kv_len, int causal);
 size_t nar_attention_workspace_elems(int batch, int kv_heads, int kv_len);
 // Keys [0, n) of `heads` cache heads (V in 32-key dim-major blocks, heads
 // kv_stride slots apart) to row-major out [heads][n][128].

@@ -16,6 +16,7 @@
 // rewritten (nar_v_blocks_kernel) into 32-key blocks stored dim-major, the
 // layout of the KV cache, in a caller-provided workspace; keys past Lk in the
 // last block are zero there (and masked in the scores).
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -83,10 +84,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(T64 ? attn:
   t.q_stride = D;
   t.out = p.out + (size_t(bh) * p.q_len + q0) * D;
   t.out_stride = D;
-  if constexpr (T64)
+  if constexpr (T64) {
+    if (p.splits > 1) {  // keys split over gridDim.z workgroups (non-causal)
+      const int nb = (p.kv_len + attn::kBlock - 1) / attn::kBlock;
+      const int per = (nb + p.splits - 1) / p.splits;
+      t.blk0 = int(blockIdx.z) * per;
+      t.blk1 = min(nb, t.blk0 + per);
+      t.part = p.part + (size_t(blockIdx.z) * p.batch * p.heads * p.q_len +
+                         size_t(bh) * p.q_len + q0) * 132;
+    }
     attn::attn_query_tile64(t, qscale, sh);
-  else
+  } else
     attn::attn_query_tile(t, qscale, sh);
+}
+
+// out[row][d] = bf16(sum_s w_s o_s[d] / sum_s w_s l_s), w_s = exp2(m_s - max m)
+// over the split partials of each query row; one thread per (row, 4 dims).
+__global__ __launch_bounds__(256) void nar_merge_kernel(const float *part, int splits, long long rows,
+                                                        uint16_t *out) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * 32)
+    return;
+  const long long row = idx / 32;
+  const int d4 = int(idx % 32) * 4;
+  float M = -__builtin_inff();
+  for (int s = 0; s < splits; ++s)
+    M = fmaxf(M, part[(s * rows + row) * 132 + 128]);
+  float L = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const float *ps = part + (s * rows + row) * 132;
+    const float m = ps[128];
+    const float w = m == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    L += w * ps[129];
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(ps + d4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] += w * v[j];
+  }
+  const uint32_t lo = uint32_t(f2bf(o[0] / L)) | (uint32_t(f2bf(o[1] / L)) << 16);
+  const uint32_t hi = uint32_t(f2bf(o[2] / L)) | (uint32_t(f2bf(o[3] / L)) << 16);
+  *reinterpret_cast<uint2 *>(out + row * 128 + d4) = uint2{lo, hi};
 }
 
 // Inverse of nar_v_blocks_kernel for a cache head: keys [0, n) of each head
@@ -121,6 +158,24 @@ hipError_t launch_v_rows(const uint16_t *vb, int kv_stride, int heads, int n, ui
   return hipGetLastError();
 }
 
+namespace {
+// Key splits for a non-causal launch whose 64-query workgroups do not fill
+// the GPU: enough to reach kTile64MinGroups, each split at least 8 blocks.
+int nar_splits(int batch, int heads, int q_len, int kv_len, int causal) {
+  const long long g64 = (long long)batch * heads * ((q_len + 63) / 64);
+  const int nb = (kv_len + attn::kBlock - 1) / attn::kBlock;
+  if (causal || g64 >= attn::kTile64MinGroups)
+    return 1;
+  const int want = int((attn::kTile64MinGroups + g64 - 1) / g64);
+  return std::max(1, std::min(want, nb / 8));
+}
+}  // namespace
+
+size_t nar_attention_part_floats(int batch, int heads, int q_len, int kv_len, int causal) {
+  const int s = nar_splits(batch, heads, q_len, kv_len, causal);
+  return s > 1 ? size_t(s) * batch * heads * q_len * 132 : 0;
+}
+
 size_t nar_attention_workspace_elems(int batch, int kv_heads, int kv_len) {
   return size_t(batch) * kv_heads * size_t((kv_len + kBlock - 1) / kBlock * kBlock) * D;
 }
@@ -138,6 +193,21 @@ hipError_t launch_nar_attention(NarAttnParams p, hipStream_t s) {
     return e;
   // scale * log2(e) as in the reference kernel (nar_attention.cpp:95)
   const float qscale = 0.08838834764831845f * 1.4426950408889634f;
+  const int splits = nar_splits(p.batch, p.heads, p.q_len, p.kv_len, p.causal);
+  if (splits > 1 && p.part &&
+      p.part_floats >= nar_attention_part_floats(p.batch, p.heads, p.q_len, p.kv_len, p.causal)) {
+    p.splits = splits;
+    hipLaunchKernelGGL(nar_attn_kernel<true>, dim3(p.batch * p.heads, (p.q_len + 63) / 64, splits),
+                       dim3(256), 0, s, p, qscale);
+    e = hipGetLastError();
+    if (e != hipSuccess)
+      return e;
+    const long long rows = (long long)p.batch * p.heads * p.q_len;
+    hipLaunchKernelGGL(nar_merge_kernel, dim3(unsigned((rows * 32 + 255) / 256)), dim3(256), 0, s,
+                       p.part, splits, rows, p.out);
+    return hipGetLastError();
+  }
+  p.splits = 1;
   if (p.batch * p.heads * ((p.q_len + 63) / 64) >= attn::kTile64MinGroups)
     hipLaunchKernelGGL(nar_attn_kernel<true>, dim3(p.batch * p.heads, (p.q_len + 63) / 64),
                        dim3(256), 0, s, p, qscale);
