@@ -306,8 +306,12 @@ int32_t yuear_op_attention_prefill(const uint16_t *dev_q,
  * the keys after each query (q_len == kv_len). query_chunk_size is validated
  * as in the reference and does not change the result (every query sees the
  * same keys in one pass). workspace: yuear_nar_attention_workspace_bytes()
- * of device memory. Runs on `stream` (a hipStream_t, NULL = default); the
- * reference's ValueError messages for invalid shapes. */
+ * of device memory. A non-causal launch too small to fill the GPU splits
+ * its keys over workgroups; the split partials come from a library pool
+ * per (device, stream). So the first such call on a stream, or one that
+ * needs a larger pool, allocates: make it outside graph capture. Runs on
+ * `stream` (a hipStream_t, NULL = default); the reference's ValueError
+ * messages for invalid shapes. */
 int64_t yuear_nar_attention_workspace_bytes(int32_t batch, int32_t kv_heads, int32_t kv_len);
 /* The acoustic stage's conditioning prefill (CachedNAR, nar.cpp:139-190):
  * the AR layers over `tokens` with causal attention (the engine's prefill;
