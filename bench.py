@@ -7,10 +7,9 @@ weights N(0, 0.02) with unit norm gains, a random prompt prefilled so that the
 timed steps are centred on KV length 4096, then greedy decoding. A step is one
 token: the device sampler (argmax) followed by the whole decode step (28 x
 [QKV GEMV, split-K attention, O GEMV, gate/up GEMV, down GEMV], lm_head GEMV),
-replayed as one hipGraph per token with no host sync between tokens. With
---decode kernels (default) the decode step is one kernel per op; with
---decode persistent it is one persistent kernel (same bits, slower today). Inputs (weights, KV cache, logits)
-are resident in HBM when the timed region starts.
+replayed as one hipGraph per token with no host sync between tokens, one
+kernel per op. Inputs (weights, KV cache, logits) are resident in HBM when the
+timed region starts.
 
 Other workloads of the same model (one JSON line each, not the headline):
   --config cfg     CFG as batch 2 (cond + uncond 512-token prompts), scale 1.5,
@@ -89,7 +88,7 @@ def gemv_shape(c, kernel):
 
 def traffic_from_profiles(kernel):
     """Measured HBM bytes per launch, if a PMC summary has been committed."""
-    name = "decode_step_3b_kv4096_pmc.md" if kernel == "decode_step" else f"gemv_{kernel}_3b_pmc.md"
+    name = f"gemv_{kernel}_3b_pmc.md"
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
@@ -97,6 +96,28 @@ def traffic_from_profiles(kernel):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def host_cpu():
+    """The CPU the baseline runs on: model name, logical CPUs of the host, and
+    the threads used -- every CPU this process may run on, capped by the
+    per-GPU CPU share the environment grants (OMP_NUM_THREADS)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", usable))
+    threads = max(1, min(usable, share))
+    note = (f"all {threads} CPUs granted to this process" if threads == usable else
+            f"{threads} threads: the CPU share per GPU (OMP_NUM_THREADS) of a host with "
+            f"{usable} usable CPUs")
+    return {"model": model, "nproc": nproc, "threads": threads, "note": note}
 
 
 def lin_params(c):
@@ -273,45 +294,6 @@ def run_batch8(args, engine, c):
             "kernels": kernels}
 
 
-PHASES = ("qkv", "attention", "merge", "o_proj", "gate_up", "down")
-
-
-def phase_timeline(tr, layers):
-    """Summary of a persistent-step trace ([phase][workgroup][ready, done],
-    100 MHz ticks): per phase type, mean over layers of the span (first
-    ready -> last done), the lag (previous phase's last done -> this phase's
-    first ready) and the tail (median done -> last done), in microseconds."""
-    import numpy as np
-    t0 = tr[tr > 0].min()
-    t = np.where(tr > 0, (tr.astype(np.float64) - t0) / 100.0, np.nan)  # us
-    rows = []
-    for i in range(t.shape[0]):
-        ready, done = t[i, :, 0], t[i, :, 1]
-        rows.append((np.nanmin(ready), np.nanmax(ready), np.nanmedian(done), np.nanmax(done)))
-    out = {"step_us": float(rows[-1][3]), "phases": {}}
-    for ph, name in enumerate(PHASES):
-        span, lag, tail = [], [], []
-        for l in range(layers):
-            i = l * 6 + ph
-            span.append(rows[i][3] - rows[i][0])
-            tail.append(rows[i][3] - rows[i][2])
-            if i > 0:
-                lag.append(rows[i][0] - rows[i - 1][3])
-        out["phases"][name] = {"span_us": round(float(np.mean(span)), 2),
-                               "lag_us": round(float(np.mean(lag)), 2) if lag else None,
-                               "tail_us": round(float(np.mean(tail)), 2)}
-    lm = rows[-1]
-    out["phases"]["lm_head"] = {"span_us": round(float(lm[3] - lm[0]), 2),
-                                "lag_us": round(float(lm[0] - rows[-2][3]), 2),
-                                "tail_us": round(float(lm[3] - lm[2]), 2)}
-    out["layer_us"] = round(float((rows[-2][3] - rows[0][0]) / layers), 2)
-    for name, v in out["phases"].items():
-        log(f"[trace] {name:9s} span {v['span_us']:7.2f} us  lag {v['lag_us']} us  "
-            f"tail {v['tail_us']:6.2f} us")
-    log(f"[trace] per layer {out['layer_us']} us, step {out['step_us']:.1f} us")
-    return out
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,14 +307,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-launches", type=int, default=112)
-    ap.add_argument("--decode", choices=("kernels", "fused", "persistent"), default="kernels",
-                    help="decode step: one kernel per op, a fused QKV+attention+o_proj "
-                         "launch per layer, or one persistent kernel")
     ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8", "nar"),
                     default="decode",
                     help="workload (decode: the headline batch-1 KV-4096 line)")
-    ap.add_argument("--phase-trace", action="store_true",
-                    help="profiling mode: per-phase timeline of one persistent decode step")
     ap.add_argument("--kernel-only", default=None,
                     help="profiling mode: only time this decode kernel (e.g. gate_up)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -381,19 +358,12 @@ def main():
     step_launches = 16
     capacity = prefill + W + K + step_launches + 8
     session = engine.session(1, capacity)
-    session.decode_path = args.decode
     rng = np.random.default_rng(args.seed)
     if args.kernel_only:
         session.prefill(0, rng.integers(0, c["vocab_size"], size=64).tolist())
         ms = session.time_kernel(args.kernel_only, args.kernel_launches)
         print(json.dumps({"kernel": args.kernel_only, "launches": args.kernel_launches,
                           "us": ms * 1e3}), flush=True)
-        return
-    if args.phase_trace:
-        session.prefill(0, rng.integers(0, c["vocab_size"], size=args.kv - 1).tolist())
-        session.time_kernel("decode_step", 4)  # warm
-        print(json.dumps(phase_timeline(session.trace_step(), c["num_hidden_layers"])),
-              flush=True)
         return
     prompt = rng.integers(0, c["vocab_size"], size=prefill).tolist()
     t = time.perf_counter()
@@ -426,38 +396,21 @@ def main():
                          "GBps": round(nbytes / (ms / 1e3) / 1e9, 1)}
         log(f"[bench] {name:9s} {ms * 1e3:8.2f} us  {nbytes / 1e6:8.2f} MB  "
             f"{nbytes / (ms / 1e3) / 1e9:7.1f} GB/s")
-    if args.decode == "persistent":
-        # the whole step is one kernel: algorithmic bytes = weights + the KV
-        # read at the current length (+ activations, < 0.01 %)
-        ms = session.time_kernel("decode_step", step_launches)
-        kv_now = session.position(0) + 1
-        nbytes = weight_bytes(c, bits) + kv_now * KV_BYTES_PER_POS
-        achieved = nbytes / (ms / 1e3) / 1e9
-        kernels["decode_step"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
-                                  "GBps": round(achieved, 1)}
-        log(f"[bench] decode_step {ms * 1e3:8.2f} us  {nbytes / 1e6:8.2f} MB  {achieved:7.1f} GB/s")
-        roofline = {"kernel": "decode_step_kernel<1,3,6,16> (whole decode step: 28 layers + "
-                              "lm_head, KV %d)" % kv_now,
-                    "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9,
-                    "unit": "GB/s", "frac": round(achieved / (PEAK_HBM / 1e9), 4),
-                    "traffic": traffic_from_profiles("decode_step")}
-    else:
-        dom = kernels["gate_up"]
-        achieved = dom["bytes"] / (dom["us"] / 1e6) / 1e9
-        name = ("gemv_kernel<1,6,2,SwiGLU> (gate/up 16384x3072" if not bits else
-                f"qgemv_kernel<1,{bits},{64 if bits == 8 else 32},3,2> (gate/up 16384x3072, "
-                f"{bits}-bit codes")
-        roofline = {"kernel": f"{name} + RMSNorm + SwiGLU)",
-                    "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9,
-                    "unit": "GB/s", "frac": round(achieved / (PEAK_HBM / 1e9), 4),
-                    "traffic": traffic_from_profiles("gate_up")}
+    dom = kernels["gate_up"]
+    achieved = dom["bytes"] / (dom["us"] / 1e6) / 1e9
+    name = ("gemv_kernel<1,6,2,SwiGLU> (gate/up 16384x3072" if not bits else
+            f"qgemv_kernel<1,{bits},{64 if bits == 8 else 32},3,2> (gate/up 16384x3072, "
+            f"{bits}-bit codes")
+    roofline = {"kernel": f"{name} + RMSNorm + SwiGLU)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM / 1e9,
+                "unit": "GB/s", "frac": round(achieved / (PEAK_HBM / 1e9), 4),
+                "traffic": traffic_from_profiles("gate_up")}
 
     cpu = None
     if not args.no_cpu:
         import cpu_ref
-        threads = min(16, os.cpu_count() or 1)
-        if "OMP_NUM_THREADS" in os.environ:
-            threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+        host = host_cpu()
+        threads = host["threads"]
         cpu_ref.lib().oracle_set_threads(threads)
         model = cpu_ref.Model(c, weights, bits=bits)
         L0 = args.kv - 1
@@ -475,7 +428,8 @@ def main():
             n += 1
         elapsed = time.perf_counter() - t
         cpu = {"value": round(n / elapsed, 4), "unit": "tokens/s", "cores": threads,
-               "kind": "port",
+               "kind": "port", "host_cpus": host["nproc"], "cpu_model": host["model"],
+               "threads_note": host["note"],
                "sample": f"{n} greedy decode steps of the same 3B model on the same weights, "
                          f"KV {L0 + 1}..{L0 + n} copied from the GPU run "
                          f"(CPU restatement of the reference graph, {elapsed:.1f} s)"}
@@ -501,7 +455,7 @@ def main():
         "config": {"workload": "3B bf16 AR decoder (H3072/F8192/28L/24:8 heads/V83968), "
                                "greedy decode at batch 1 centred on KV length 4096",
                    "batch": 1, "kv_len": args.kv, "prefill_tokens": prefill,
-                   "mean_kv_len": mean_kv, "decode": args.decode,
+                   "mean_kv_len": mean_kv, "decode": "kernels",
                    "parallelism": "single-gpu"},
         "step_roofline": {"bytes_per_step": int(step_bytes),
                           "achieved_GBps": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),

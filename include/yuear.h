@@ -189,32 +189,6 @@ yuear_status yuear_session_write_logits(yuear_session *session,
                                         const uint16_t *logits, char **error_json);
 yuear_status yuear_session_set_position(yuear_session *session, int32_t branch,
                                         int32_t position, char **error_json);
-/* Decode-step execution: YUEAR_DECODE_KERNELS replays one kernel per op
- * (QKV, attention, O, gate/up, down per layer, lm_head); YUEAR_DECODE_PERSISTENT
- * runs the whole step as one persistent kernel (hidden sizes 3072/2048 with
- * 8 kv heads, 1 or 2 branches); YUEAR_DECODE_FUSED runs QKV + attention +
- * o_proj of a layer as one launch (1 or 2 branches, query heads per kv head
- * 2-4, hidden 256/2048/3072 equal to heads x 128), then gate/up and down.
- * All produce the same bits. Engines with quantized linears use
- * YUEAR_DECODE_KERNELS only. They replace the per-op graph of GraphAR
- * (cuda_graph.py:43-240). The default is YUEAR_DECODE_KERNELS (the fastest
- * measured on MI355X); YUEAR_DECODE=persistent|fused in the environment
- * when the session begins selects another where available. */
-#define YUEAR_DECODE_KERNELS 0
-#define YUEAR_DECODE_PERSISTENT 1
-#define YUEAR_DECODE_FUSED 2
-yuear_status yuear_session_set_decode_path(yuear_session *session, int32_t path,
-                                           char **error_json);
-int32_t yuear_session_decode_path(const yuear_session *session);
-/* Profiling hook: runs one persistent decode step with its phase trace on
- * and restores the positions afterwards (the slot written stays invisible).
- * trace_out receives (layers * 6 + 1) * grid * 2 timestamps of the 100 MHz
- * device clock, [layer * 6 + phase][workgroup][ready, done], phases QKV,
- * attention, merge, O, gate/up, down, then the lm_head; 0 where a workgroup
- * had no task. *grid_out receives the workgroup count. */
-yuear_status yuear_session_trace_step(yuear_session *session, uint64_t *trace_out,
-                                      int64_t capacity, int32_t *grid_out,
-                                      char **error_json);
 /* One decoder layer decode step (ar.cpp:265-298) on explicit hidden rows
  * x_in [branches][H], appending at each branch's position (advanced by 1). */
 yuear_status yuear_session_layer_step(yuear_session *session, int32_t layer,
@@ -242,8 +216,7 @@ yuear_status yuear_session_time_generate(yuear_session *session,
 /* Average device time of one kernel of the decode step, launched `launches`
  * times back to back on the session stream (GEMVs cycle through the layers
  * so weights stream from HBM). kernel: "qkv", "attention", "o_proj",
- * "gate_up", "down", "lm_head", or "decode_step" (the whole persistent step;
- * needs launches + 1 free slots, positions are restored afterwards). */
+ * "gate_up", "down" or "lm_head". */
 yuear_status yuear_session_time_kernel(yuear_session *session,
                                        const char *kernel, int32_t launches,
                                        double *ms_per_launch, char **error_json);

@@ -202,15 +202,6 @@ def test_quantized_engine_cfg_pair_and_batched_sequences(qtiny):
             assert within(got[bi], model.step(toks[bi], caches[bi])).all(), (branches, bi)
 
 
-def test_quantized_engine_is_kernels_path_only(qtiny):
-    _, engine, _, _ = qtiny
-    s = engine.session(1, 16)
-    for path in ("fused", "persistent"):
-        with pytest.raises(ValueError, match="quantized"):
-            s.decode_path = path
-    assert s.decode_path == "kernels"
-
-
 def test_quantized_engine_rejects_bf16_linears(yuear_lib):
     w = yuear_lib.random_weights(TINY, seed=2)
     with pytest.raises(ValueError, match="Missing AR tensor|Incompatible AR tensor"):

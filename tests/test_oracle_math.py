@@ -90,6 +90,67 @@ def test_shared_uniform_is_in_open_unit_interval_and_flat(oracle):
     assert lib.oracle_uniform(17, 0, 0) != lib.oracle_uniform(2**40 + 17, 0, 0)
 
 
+# ---- categorical draw ----
+# sampling.cpp:128-132 draws categorical(log(softmax(scores))): token i with
+# probability softmax(scores)_i. The oracle's draw (shared uniforms, argmax of
+# s_i - log(-log u_i)) must produce exactly those frequencies after
+# distribution() has applied the temperature (sampling.cpp:76-80).
+
+def _chi2_pvalue(counts, probs):
+    from scipy.stats import chisquare
+    counts = np.asarray(counts, dtype=np.float64)
+    return chisquare(counts, counts.sum() * np.asarray(probs, dtype=np.float64)).pvalue
+
+
+def _draw_counts(oracle, scores, n_draws, key_of=None):
+    """Token counts over (seed, step) pairs; key_of(scores, u) replaces the
+    oracle's draw by a variant computed from the same uniforms."""
+    lib = oracle.lib()
+    counts = np.zeros(scores.size, dtype=np.int64)
+    finite = np.isfinite(scores)
+    for j in range(n_draws):
+        seed, step = 9000 + j // 250, j % 250
+        if key_of is None:
+            tok = oracle.draw(scores, 1.0, seed, step)
+        else:
+            u = np.array([lib.oracle_uniform(seed, step, i) for i in range(scores.size)],
+                         dtype=np.float64)
+            key = np.where(finite, key_of(scores.astype(np.float64), u), -np.inf)
+            tok = int(np.argmax(key))
+        counts[tok] += 1
+    return counts
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_categorical_draw_follows_softmax(oracle, temperature):
+    logits = bf([1.5, 0.25, -0.75, 2.0, 0.0, -30.0])
+    sampling = oracle.sampling_struct(temperature=temperature, top_p=1.0, top_k=6,
+                                      repetition_penalty=1.0, penalty_window=0, min_tokens=0)
+    scores = oracle.distribution(logits, sampling, [], 0)
+    lf = f(logits).astype(np.float64)
+    assert np.allclose(scores, lf / temperature, rtol=1e-6)  # temperature applied once
+    p = np.exp(lf / temperature - (lf / temperature).max())
+    p /= p.sum()
+    n = 40000
+    counts = _draw_counts(oracle, scores, n)
+    assert _chi2_pvalue(counts[:5], p[:5] / p[:5].sum()) > 1e-3, (counts, p * n)
+    # slips the test must catch, drawn from the same uniforms: a sign-flipped
+    # Gumbel term, and the temperature applied a second time
+    flipped = _draw_counts(oracle, scores, 8000, lambda s, u: s + np.log(-np.log(u)))
+    assert _chi2_pvalue(flipped[:5], p[:5] / p[:5].sum()) < 1e-6
+    if temperature != 1.0:
+        twice = _draw_counts(oracle, scores, 8000,
+                             lambda s, u: s / temperature - np.log(-np.log(u)))
+        assert _chi2_pvalue(twice[:5], p[:5] / p[:5].sum()) < 1e-6
+
+
+def test_categorical_draw_skips_masked_rows_and_greedy_takes_lowest_index(oracle):
+    scores = np.array([-np.inf, 0.5, -np.inf, 0.5, -np.inf], dtype=np.float32)
+    seen = {oracle.draw(scores, 1.0, 5, s) for s in range(400)}
+    assert seen == {1, 3}
+    assert oracle.draw(scores, 0.0, 5, 0) == 1  # argmax ties: lowest index
+
+
 # ---- model ops ----
 
 def test_rms_norm_special_cases(oracle):

@@ -1,8 +1,9 @@
 // Split-K flash-decode attention for one layer on gfx950 (head_dim 128),
-// one kernel per layer: grid (max_splits, Hkv, batch), 256 threads; the
-// workgroup body is attn_block.h (shared with the fused layer kernel). The
-// chunk length is derived on device from pos[b], so one captured graph
-// serves every KV length up to capacity.
+// one kernel per layer: a one-dimensional grid of max_splits * batch * Hkv
+// workgroups of 256 threads, block = split * (batch * Hkv) + bh (the splits
+// of one (branch, kv head) spread over the XCDs). The workgroup body is
+// attn_block.h. The chunk length is derived on device from pos[b], so one
+// captured graph serves every KV length up to capacity.
 #include <cmath>
 
 #include "attn_block.h"
@@ -19,15 +20,16 @@ constexpr int kWaves = 4;  // 128 keys per pass (8 waves measured no faster on M
 template <int G, int W>
 __global__ __launch_bounds__(64 * W) void attn_decode_kernel(AttnDecodeParams p, float scale) {
   __shared__ AttnShared<G, W> sm;
-  attn_block<G, W, false>(p, scale, blockIdx.x, blockIdx.y, blockIdx.z, int(gridDim.x), sm,
-                          WordIO{});
+  const int nbh = p.batch * p.kv_heads;
+  attn_block<G, W>(p, scale, int(blockIdx.x) / nbh, int(blockIdx.x) % nbh, p.max_splits, sm);
 }
 
 template <int G>
 hipError_t launch_g(const AttnDecodeParams &p, hipStream_t s) {
   const float scale = float(std::pow(double(D), -0.5));  // ar.cpp:283
-  hipLaunchKernelGGL((attn_decode_kernel<G, kWaves>), dim3(p.max_splits, p.kv_heads, p.batch),
-                     dim3(64 * kWaves), 0, s, p, scale);
+  hipLaunchKernelGGL((attn_decode_kernel<G, kWaves>),
+                     dim3(p.max_splits * p.batch * p.kv_heads), dim3(64 * kWaves), 0, s, p,
+                     scale);
   return hipGetLastError();
 }
 
@@ -47,6 +49,16 @@ hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s) {
   case 8: return launch_g<8>(p, s);
   }
   return hipErrorInvalidValue;
+}
+
+int attn_decode_splits(int batch, int kv_heads, int kv_stride) {
+  // One 128-key pass per workgroup at the session's capacity (every K/V
+  // operand of a split in flight at once), capped so that a launch stays
+  // within about 512 workgroups; never more splits than 32-key blocks.
+  const int nbh = batch * kv_heads;
+  const int passes = (kv_stride + 32 * kWaves - 1) / (32 * kWaves);
+  const int cap = std::max(2, 512 / nbh);
+  return std::max(1, std::min({kAttnMaxSplits, cap, passes, kv_stride / attn::kBlock}));
 }
 
 }  // namespace yuear

@@ -20,13 +20,24 @@ YHD float bf2f(uint16_t b) { return __builtin_bit_cast(float, uint32_t(b) << 16)
 YHD float bflo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 YHD float bfhi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
-// fp32 -> bf16, round to nearest even (quiet NaN preserved).
-YHD uint16_t f2bf(float f) {
+// fp32 -> bf16, round to nearest even (quiet NaN preserved), in integer
+// operations.
+YHD uint16_t f2bf_int(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7fffffffu) > 0x7f800000u)
     return uint16_t((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return uint16_t(u >> 16);
+}
+// The same rounding; on gfx950 the device form is one v_cvt_pk_bf16_f32,
+// which equals f2bf_int on all 2^32 inputs (denormals, infinities and NaNs
+// included, checked exhaustively on MI355X) in a dozen fewer VALU operations.
+YHD uint16_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+#else
+  return f2bf_int(f);
+#endif
 }
 YHD float rbf(float f) { return bf2f(f2bf(f)); }
 

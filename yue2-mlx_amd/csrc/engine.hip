@@ -32,7 +32,6 @@
 #include "abi_util.h"
 #include "attn_core.h"
 #include "common.h"
-#include "decode.h"
 #include "kernels.h"
 
 namespace yuear {
@@ -286,24 +285,6 @@ struct yuear_session {
   int32_t *pin_tok = nullptr;
   uint16_t *pin_logits = nullptr;
   std::vector<void *> allocations;
-  // persistent decode step (decode.hip): one launch per token
-  int decode_path = 0;  // YUEAR_DECODE_KERNELS, _PERSISTENT or _FUSED
-  int decode_grid = 0;  // co-resident workgroups; 0: shape not supported
-  int decode_spins = 1 << 20;  // bounded-wait polls (YUEAR_DECODE_SPIN_LIMIT)
-  int32_t *dsync = nullptr;     // counters + error word, zero between launches
-  DecodeLayer *dlayers = nullptr;
-  // activation words of the persistent step (decode.h)
-  uint32_t *dxs = nullptr, *dqkv = nullptr, *dattn = nullptr, *dact = nullptr;
-  uint32_t *dpart_o = nullptr, *dpart_ml = nullptr;
-  int32_t *pin_err = nullptr;
-  // fused QKV + attention + o_proj layer kernel (fused.hip): per-layer
-  // activation words, the step counter that tags them (advanced by the
-  // lm_head) and the sticky error word of its bounded waits
-  bool fused_ok = false;
-  uint32_t *fqkv = nullptr, *fattn = nullptr;
-  u32x4 *fpart = nullptr;
-  int32_t *fsync = nullptr;  // [0] step counter, [1] error word
-  long long fused_ticks = 2000000;  // 20 ms per wait (YUEAR_FUSED_WAIT_US)
   hipGraphExec_t step_exec = nullptr;
   hipGraph_t step_graph = nullptr;
   hipGraphExec_t gen_exec = nullptr;  // sampler + step, for timed loops
@@ -319,7 +300,6 @@ struct yuear_session {
     for (void *p : allocations) (void)hipFree(p);
     if (pin_tok) (void)hipHostFree(pin_tok);
     if (pin_logits) (void)hipHostFree(pin_logits);
-    if (pin_err) (void)hipHostFree(pin_err);
     if (stream) (void)hipStreamDestroy(stream);
   }
   template <class T> T *alloc(size_t n) {
@@ -642,11 +622,10 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.attn = S.alloc<uint16_t>(size_t(branches) * c.Hq * c.D);
   S.act = S.alloc<uint16_t>(size_t(branches) * c.F);
   S.logits = S.alloc<uint16_t>(size_t(branches) * S.phase.stride());
-  // split-K: about 192 workgroups over all branches and kv heads (24 splits
-  // at batch 1 with 8 kv heads, 3 at batch 8), never more splits than 32-key
-  // blocks; measured best on MI355X at KV 1k-8k. YUEAR_ATTN_SPLITS overrides.
+  // split-K: one 128-key pass per workgroup at the session's capacity, at
+  // most ~512 workgroups (attn_decode_splits); YUEAR_ATTN_SPLITS overrides.
   {
-    int splits = (192 + branches * c.Hkv - 1) / (branches * c.Hkv);
+    int splits = attn_decode_splits(branches, c.Hkv, S.kv_stride);
     if (const char *env = std::getenv("YUEAR_ATTN_SPLITS"))
       splits = std::atoi(env);
     S.max_splits = std::max(1, std::min({64, splits, S.kv_stride / attn::kBlock}));
@@ -686,74 +665,6 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_tok), size_t(kContext + 16) * 4));
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_logits),
                      size_t(branches) * S.phase.stride() * 2));
-  HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_err), 4));
-  // persistent decode step: needs every workgroup of its grid resident at
-  // once; the grid is sized from the occupancy query (YUEAR_DECODE_WG_PER_CU
-  // caps the workgroups per CU, default 2)
-  const int occ = E->bits ? 0 : decode_occupancy(c.H, c.F, c.Hq, c.Hkv, branches);
-  if (occ > 0) {
-    int cus = 0;
-    HIPC(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, E->device));
-    int per_cu = 2;
-    if (const char *env = std::getenv("YUEAR_DECODE_WG_PER_CU"))
-      per_cu = std::max(1, std::atoi(env));
-    S.decode_grid = std::min(per_cu, occ) * cus;
-    if (const char *env = std::getenv("YUEAR_DECODE_SPIN_LIMIT"))
-      S.decode_spins = std::max(0, std::atoi(env));
-    const size_t words = decode_sync_words(c.layers);
-    S.dsync = S.alloc<int32_t>(words);
-    HIPC(hipMemsetAsync(S.dsync, 0, words * 4, S.stream));
-    const size_t L = c.layers, Bn = branches;
-    const size_t parts = Bn * c.Hkv * S.max_splits * G;
-    // zero words carry tag 0, which no launch uses
-    const size_t act_words = (2 * L + 1) * Bn * c.H + L * Bn * (c.qkv() + c.Hq * c.D + c.F) +
-                             L * parts * (2 * c.D + 4);
-    uint32_t *act_base = S.alloc<uint32_t>(act_words);
-    HIPC(hipMemsetAsync(act_base, 0, act_words * 4, S.stream));
-    S.dxs = act_base;
-    S.dqkv = S.dxs + (2 * L + 1) * Bn * c.H;
-    S.dattn = S.dqkv + L * Bn * c.qkv();
-    S.dact = S.dattn + L * Bn * c.Hq * c.D;
-    S.dpart_o = S.dact + L * Bn * c.F;
-    S.dpart_ml = S.dpart_o + L * parts * 2 * c.D;
-    std::vector<DecodeLayer> table(c.layers);
-    for (int l = 0; l < c.layers; ++l) {
-      const LayerW &L = E->layers[l];
-      table[l] = DecodeLayer{L.input_ln, L.post_ln, c.qk_norm ? L.q_norm : nullptr,
-                             c.qk_norm ? L.k_norm : nullptr, L.qkv, L.o, L.gu, L.down};
-    }
-    S.dlayers = S.alloc<DecodeLayer>(c.layers);
-    HIPC(hipMemcpyAsync(S.dlayers, table.data(), table.size() * sizeof(DecodeLayer),
-                        hipMemcpyHostToDevice, S.stream));
-  }
-  // step counter (advanced by the lm_head of every decode step) and the
-  // sticky error word of the fused path's bounded waits; its tagged split
-  // partials of the attention (counter-free merge), shared by all layers
-  S.fsync = S.alloc<int32_t>(2);
-  HIPC(hipMemsetAsync(S.fsync, 0, 8, S.stream));
-  {
-    const size_t pv = size_t(branches) * c.Hkv * S.max_splits * (G * (c.D / 2) + G);
-    S.fpart = S.alloc<u32x4>(pv);  // zero: tag 0, which no launch uses
-    HIPC(hipMemsetAsync(S.fpart, 0, pv * 16, S.stream));
-  }
-  if (const char *env = std::getenv("YUEAR_FUSED_WAIT_US"))
-    S.fused_ticks = std::max(0LL, std::atoll(env)) * 100;
-  // fused layer kernel (1-2 branches)
-  S.fused_ok = E->bits == 0 && fused_layer_supported(c.H, c.Hq, c.Hkv, c.D, branches);
-  if (S.fused_ok) {
-    const size_t words = size_t(c.layers) * branches * (c.qkv() + c.Hq * c.D);
-    S.fqkv = S.alloc<uint32_t>(words);  // zero words carry tag 0, which no step uses
-    S.fattn = S.fqkv + size_t(c.layers) * branches * c.qkv();
-    HIPC(hipMemsetAsync(S.fqkv, 0, words * 4, S.stream));
-  }
-  S.decode_path = YUEAR_DECODE_KERNELS;
-  if (const char *env = std::getenv("YUEAR_DECODE")) {
-    const std::string v = env;
-    if (v == "persistent" && S.dsync)
-      S.decode_path = YUEAR_DECODE_PERSISTENT;
-    else if (v == "fused" && S.fused_ok)
-      S.decode_path = YUEAR_DECODE_FUSED;
-  }
   HIPC(hipStreamSynchronize(S.stream));
 }
 
@@ -775,7 +686,6 @@ void set_quant(GemvParams &g, int bits, const uint32_t *codes, const uint32_t *g
 }
 
 // decode kernels of one layer on S.x (all branches)
-void enqueue_fused_qkv_attn_o(yuear_session &S, int l, bool embed_first);
 void enqueue_ffn(yuear_session &S, int l);
 
 void enqueue_layer(yuear_session &S, int l, bool embed_first) {
@@ -783,11 +693,6 @@ void enqueue_layer(yuear_session &S, int l, bool embed_first) {
   const Config &c = E.cfg;
   const LayerW &L = E.layers[l];
   hipStream_t st = S.stream;
-  if (S.decode_path == YUEAR_DECODE_FUSED) {
-    enqueue_fused_qkv_attn_o(S, l, embed_first);
-    enqueue_ffn(S, l);
-    return;
-  }
   GemvParams q;
   q.w = L.qkv;
   set_quant(q, E.bits, L.qqkv, L.gqkv);
@@ -889,69 +794,6 @@ void enqueue_ffn(yuear_session &S, int l) {
   HIPC(launch_gemv(d, st));
 }
 
-// QKV + attention + o_proj of layer l as one launch (fused.hip)
-void enqueue_fused_qkv_attn_o(yuear_session &S, int l, bool embed_first) {
-  yuear_engine &E = *S.e;
-  const Config &c = E.cfg;
-  const LayerW &L = E.layers[l];
-  FusedLayerParams f;
-  GemvParams &q = f.q;
-  q.w = L.qkv;
-  q.n = c.qkv();
-  q.k = c.H;
-  q.batch = S.B;
-  q.x = S.x;
-  q.x_stride = c.H;
-  if (embed_first) {
-    q.embed = E.embed;
-    q.tokens = S.tok;
-    q.embed_rows = c.V;
-  }
-  q.norm_w = L.input_ln;
-  q.eps = c.eps;
-  q.y_stride = c.qkv();
-  AttnDecodeParams &a = f.a;
-  a.q_norm = c.qk_norm ? L.q_norm : nullptr;
-  a.k_norm = c.qk_norm ? L.k_norm : nullptr;
-  a.eps = c.eps;
-  a.rope_cos = E.rope_cos;
-  a.rope_sin = E.rope_sin;
-  a.k_cache = S.kc + S.layer_kv_offset(l, 0);
-  a.v_cache = S.vc + S.layer_kv_offset(l, 0);
-  a.pos = S.pos;
-  a.heads = c.Hq;
-  a.kv_heads = c.Hkv;
-  a.head_dim = c.D;
-  a.capacity = S.kv_stride;
-  a.batch = S.B;
-  a.max_splits = S.max_splits;
-  a.part_o = S.part_o;
-  a.part_ml = S.part_ml;
-  a.counters = S.counters;
-  GemvParams &o = f.o;
-  o.w = L.o;
-  o.n = c.H;
-  o.k = c.Hq * c.D;
-  o.batch = S.B;
-  o.x_stride = c.Hq * c.D;
-  o.y = S.x;
-  o.y_stride = c.H;
-  o.epilogue = kEpiResidual;
-  if (embed_first) {  // the residual stream of the first layer is the embedding row
-    o.embed = E.embed;
-    o.tokens = S.tok;
-    o.embed_rows = c.V;
-  }
-  f.qkv_words = S.fqkv + size_t(l) * S.B * c.qkv();
-  f.attn_words = S.fattn + size_t(l) * S.B * c.Hq * c.D;
-  f.part = S.fpart;
-  f.layer = l;
-  f.epoch = S.fsync;
-  f.err = S.fsync + 1;
-  f.max_ticks = S.fused_ticks;
-  HIPC(launch_fused_layer(f, S.stream));
-}
-
 void enqueue_one(yuear_session &S, const std::string &which, int l);
 
 void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, uint16_t *out,
@@ -976,8 +818,6 @@ void enqueue_head(yuear_session &S, const uint16_t *x, int batch, int x_stride, 
   h.seg0_len = S.phase.seg0_len;
   h.seg1_start = S.phase.seg1_start;
   h.advance = advance;
-  if (advance)  // a decode step: the step counter that tags the fused path's words
-    h.epoch = S.fsync;
   HIPC(launch_gemv(h, S.stream));
 }
 
@@ -1028,36 +868,8 @@ void enqueue_one(yuear_session &S, const std::string &which, int l) {
   HIPC(launch_gemv(g, S.stream));
 }
 
-DecodeParams decode_params(yuear_session &S) {
-  yuear_engine &E = *S.e;
-  const Config &c = E.cfg;
-  DecodeParams p;
-  p.H = c.H; p.F = c.F; p.Hq = c.Hq; p.Hkv = c.Hkv; p.B = S.B; p.n_layers = c.layers;
-  p.vocab = c.V;
-  p.eps = c.eps;
-  p.attn_scale = float(std::pow(double(c.D), -0.5));  // ar.cpp:283
-  p.embed = E.embed; p.lm_head = E.lm_head; p.final_norm = E.final_norm;
-  p.rope_cos = E.rope_cos; p.rope_sin = E.rope_sin;
-  p.layers = S.dlayers;
-  p.kc = S.kc; p.vc = S.vc; p.cap = S.kv_stride;
-  p.pos = S.pos; p.tok = S.tok;
-  p.xs = S.dxs; p.qkv = S.dqkv; p.qkv_stride = c.qkv(); p.attn = S.dattn; p.act = S.dact;
-  p.part_o = S.dpart_o; p.part_ml = S.dpart_ml; p.max_splits = S.max_splits;
-  p.logits = S.logits; p.ls = S.phase.stride(); p.n_logits = S.phase.size;
-  p.seg0_start = S.phase.seg0_start; p.seg0_len = S.phase.seg0_len;
-  p.seg1_start = S.phase.seg1_start;
-  p.sync = S.dsync;
-  p.grid = S.decode_grid;
-  p.max_spins = S.decode_spins;
-  return p;
-}
-
 // whole decode step: tok -> logits, pos += 1
 void enqueue_step(yuear_session &S) {
-  if (S.decode_path == YUEAR_DECODE_PERSISTENT) {
-    HIPC(launch_decode_step(decode_params(S), S.stream));
-    return;
-  }
   for (int l = 0; l < S.e->cfg.layers; ++l)
     enqueue_layer(S, l, l == 0);
   enqueue_head(S, S.x, S.B, S.e->cfg.H, S.logits, S.pos);
@@ -1077,36 +889,6 @@ void ensure_step_graph(yuear_session &S) {
   }
   HIPC(hipStreamEndCapture(S.stream, &S.step_graph));
   HIPC(hipGraphInstantiate(&S.step_exec, S.step_graph, nullptr, nullptr, 0));
-}
-
-// The persistent step and the fused layer kernel report an expired dependency
-// wait through a sticky word: the results since the last check are invalid.
-// Synchronises the session stream.
-void check_decode(yuear_session &S) {
-  if (S.fsync) {
-    HIPC(hipMemcpyAsync(S.pin_err, S.fsync + 1, 4, hipMemcpyDeviceToHost, S.stream));
-    HIPC(hipStreamSynchronize(S.stream));
-    if (*S.pin_err != 0) {
-      HIPC(hipMemsetAsync(S.fsync + 1, 0, 4, S.stream));
-      HIPC(hipStreamSynchronize(S.stream));
-      throw Error("RuntimeError",
-                  "decode step: a dependency wait expired; the decoded state is invalid");
-    }
-  }
-  if (!S.dsync)
-    return;
-  HIPC(hipMemcpyAsync(S.pin_err, S.dsync + kSyncError, 4, hipMemcpyDeviceToHost, S.stream));
-  HIPC(hipStreamSynchronize(S.stream));
-  if (*S.pin_err != 0) {
-    // reset everything but the epoch (activation words keep their tags)
-    HIPC(hipMemsetAsync(S.dsync, 0, kSyncEpoch * 4, S.stream));
-    HIPC(hipMemsetAsync(S.dsync + kSyncEpoch + 1, 0,
-                        (decode_sync_words(S.e->cfg.layers) - kSyncEpoch - 1) * 4, S.stream));
-    HIPC(hipStreamSynchronize(S.stream));
-    throw Error("RuntimeError",
-                "persistent decode step: a dependency wait expired (workgroups not co-resident); "
-                "the decoded state is invalid");
-  }
 }
 
 void drop_graphs(yuear_session &S) {
@@ -1227,12 +1009,10 @@ void step(yuear_session &S, const int32_t *tokens, uint16_t *logits_out) {
     HIPC(hipMemcpyAsync(S.pin_logits, S.logits, size_t(S.B) * ls * 2, hipMemcpyDeviceToHost,
                         S.stream));
     HIPC(hipStreamSynchronize(S.stream));
-    check_decode(S);
     for (int b = 0; b < S.B; ++b)
       std::memcpy(logits_out + b * n, S.pin_logits + b * ls, n * 2);
   } else {
     HIPC(hipStreamSynchronize(S.stream));
-    check_decode(S);
   }
 }
 
@@ -1295,9 +1075,18 @@ namespace {
 // calls on one stream are ordered and may share it, calls on different
 // streams or devices never do. Grown on demand (the stream is synchronised
 // before the smaller buffer is freed), kept until the process ends.
+// Scratch of the op-level entry points, one buffer per (device, stream). A
+// buffer handed out is never freed: a launch still in flight, or a graph
+// captured on that stream, may hold its address. A request larger than the
+// current buffer retires it (kept until the process ends) and allocates
+// max(request, 2 x current) rounded to a power of two, so a growing caller
+// retires O(log size) buffers and never synchronises. Growth while the
+// stream is being captured is refused (hipErrorStreamCaptureUnsupported):
+// make the largest call once before capturing.
 struct OpPool {
   std::mutex mu;
   std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> bufs;
+  std::vector<void *> retired;
   hipError_t get(hipStream_t s, size_t bytes, void **out, bool *fresh) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -1307,15 +1096,20 @@ struct OpPool {
     auto &b = bufs[{dev, s}];
     *fresh = false;
     if (bytes > b.second) {
-      if (b.first) {
-        if ((e = hipStreamSynchronize(s)) != hipSuccess)
-          return e;
-        (void)hipFree(b.first);
-      }
-      b = {nullptr, 0};
-      if ((e = hipMalloc(&b.first, bytes)) != hipSuccess)
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess)
         return e;
-      b.second = bytes;
+      if (cs != hipStreamCaptureStatusNone)
+        return hipErrorStreamCaptureUnsupported;
+      size_t size = 256;
+      while (size < std::max(bytes, 2 * b.second))
+        size <<= 1;
+      void *p = nullptr;
+      if ((e = hipMalloc(&p, size)) != hipSuccess)
+        return e;
+      if (b.first)
+        retired.push_back(b.first);
+      b = {p, size};
       *fresh = true;
     }
     *out = b.first;
@@ -1524,68 +1318,6 @@ yuear_status yuear_session_set_position(yuear_session *S, int32_t branch, int32_
   });
 }
 
-yuear_status yuear_session_set_decode_path(yuear_session *S, int32_t path, char **error_json) {
-  return guarded(error_json, [&] {
-    if (!S || (path != YUEAR_DECODE_KERNELS && path != YUEAR_DECODE_PERSISTENT &&
-               path != YUEAR_DECODE_FUSED))
-      invalid("decode path must be YUEAR_DECODE_KERNELS, YUEAR_DECODE_PERSISTENT or "
-              "YUEAR_DECODE_FUSED");
-    if (path != YUEAR_DECODE_KERNELS && S->e->bits)
-      invalid("the persistent and fused decode paths read bf16 weights; this engine's "
-              "linears are quantized");
-    if (path == YUEAR_DECODE_PERSISTENT && !S->dsync)
-      invalid("the persistent decode step is not available for this model shape / branch count");
-    if (path == YUEAR_DECODE_FUSED && !S->fused_ok)
-      invalid("the fused decode layer is not available for this model shape / branch count");
-    if (path != S->decode_path) {
-      drop_graphs(*S);
-      // steps of the persistent path do not advance the step counter: move
-      // it on so that no word or partial of an earlier step carries the next tag
-      int32_t epoch = 0;
-      HIPC(hipMemcpy(&epoch, S->fsync, 4, hipMemcpyDeviceToHost));
-      epoch += 1;
-      HIPC(hipMemcpy(S->fsync, &epoch, 4, hipMemcpyHostToDevice));
-      S->decode_path = path;
-    }
-  });
-}
-
-int32_t yuear_session_decode_path(const yuear_session *S) { return S ? S->decode_path : -1; }
-
-yuear_status yuear_session_trace_step(yuear_session *S, uint64_t *trace_out, int64_t capacity,
-                                      int32_t *grid_out, char **error_json) {
-  return guarded(error_json, [&] {
-    if (!S || !trace_out || !grid_out)
-      invalid("session and outputs are required");
-    if (!S->dsync)
-      invalid("the persistent decode step is not available for this session");
-    for (int b = 0; b < S->B; ++b)
-      if (S->host_pos[b] + 1 > S->cap)
-        invalid("trace_step needs a free slot");
-    const size_t n = (size_t(S->e->cfg.layers) * kPhases + 1) * S->decode_grid * 2;
-    if (capacity < int64_t(n))
-      invalid("trace buffer too small: need " + std::to_string(n) + " entries");
-    DecodeParams dp = decode_params(*S);
-    unsigned long long *dev = nullptr;
-    HIPC(hipMalloc(&dev, n * 8));
-    const auto release = [&] { (void)hipFree(dev); };
-    try {
-      HIPC(hipMemsetAsync(dev, 0, n * 8, S->stream));
-      dp.trace = dev;
-      HIPC(launch_decode_step(dp, S->stream));
-      HIPC(hipStreamSynchronize(S->stream));
-      HIPC(hipMemcpy(trace_out, dev, n * 8, hipMemcpyDeviceToHost));
-      set_device_pos(*S);  // the traced step leaves the positions unchanged
-      check_decode(*S);
-    } catch (...) {
-      release();
-      throw;
-    }
-    release();
-    *grid_out = S->decode_grid;
-  });
-}
-
 yuear_status yuear_session_layer_step(yuear_session *S, int32_t layer, const uint16_t *x_in,
                                       uint16_t *x_out, char **error_json) {
   return guarded(error_json, [&] {
@@ -1631,7 +1363,6 @@ yuear_status yuear_session_time_steps(yuear_session *S, int32_t steps, double *m
     (void)hipEventDestroy(e1);
     for (int b = 0; b < S->B; ++b)
       S->host_pos[b] += steps;
-    check_decode(*S);
     *ms_per_step = double(ms) / steps;
   });
 }
@@ -1699,7 +1430,6 @@ yuear_status yuear_session_time_generate(yuear_session *S, const yuear_sampling 
     (void)hipEventDestroy(e1);
     for (int b = 0; b < S->B; ++b)
       S->host_pos[b] += steps;
-    check_decode(*S);
     *ms_per_step = double(ms) / steps;
     if (tokens_out)
       HIPC(hipMemcpy(tokens_out, S->history + first, size_t(steps) * 4, hipMemcpyDeviceToHost));
@@ -1715,35 +1445,6 @@ yuear_status yuear_session_time_kernel(yuear_session *S, const char *kernel, int
     for (int b = 0; b < S->B; ++b)
       if (which == "attention" && S->host_pos[b] >= S->cap)
         invalid("attention timing needs a free slot");
-    if (which == "decode_step") {
-      // back-to-back persistent steps from the current positions; the
-      // positions are restored afterwards (the slots written stay invisible)
-      if (!S->dsync)
-        invalid("the persistent decode step is not available for this session");
-      for (int b = 0; b < S->B; ++b)
-        if (S->host_pos[b] + launches + 1 > S->cap)
-          invalid("decode_step timing needs launches + 1 free slots");
-      const DecodeParams dp = decode_params(*S);
-      HIPC(launch_decode_step(dp, S->stream));
-      HIPC(hipStreamSynchronize(S->stream));
-      set_device_pos(*S);
-      hipEvent_t e0, e1;
-      HIPC(hipEventCreate(&e0));
-      HIPC(hipEventCreate(&e1));
-      HIPC(hipEventRecord(e0, S->stream));
-      for (int i = 0; i < launches; ++i)
-        HIPC(launch_decode_step(dp, S->stream));
-      HIPC(hipEventRecord(e1, S->stream));
-      HIPC(hipEventSynchronize(e1));
-      float ms = 0.f;
-      HIPC(hipEventElapsedTime(&ms, e0, e1));
-      (void)hipEventDestroy(e0);
-      (void)hipEventDestroy(e1);
-      set_device_pos(*S);
-      check_decode(*S);
-      *ms_per_launch = double(ms) / launches;
-      return;
-    }
     enqueue_one(*S, which, 0);  // validates the name, warms the code object
     HIPC(hipStreamSynchronize(S->stream));
     hipEvent_t e0, e1;
@@ -1888,7 +1589,6 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
     while (consumed < launched && !eos && !cancelled)
       consume();
     HIPC(hipStreamSynchronize(S->stream));
-    check_decode(*S);
     if (cancelled)
       throw Error("InterruptedError", "Cancelled during " + phase);
     const double seconds = since(t0);

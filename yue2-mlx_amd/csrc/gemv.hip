@@ -1,6 +1,6 @@
 // bf16 GEMV for batch 1..8 decode projections on gfx950: one kernel per
-// projection (the workgroup body is gemv_core.h, shared with the fused layer
-// kernel). Batches of 3..8 rows go to the MFMA form (gemv_mfma.hip).
+// projection (the workgroup body is gemv_core.h). Batches of 3..8 rows go to
+// the MFMA form (gemv_mfma.hip).
 #include "common.h"
 #include "gemv_core.h"
 #include "kernels.h"
@@ -13,7 +13,7 @@ template <int B, int KC, int R, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   extern __shared__ u32x4 xs[];  // [B][nch] activation chunks (bf16 x 8)
   __shared__ float red[B][4];
-  gemv_block<B, KC, R, EPI, kGemvPlain>(p, blockIdx.x, xs, red, WordIO{});
+  gemv_block<B, KC, R, EPI>(p, blockIdx.x, xs, red);
 }
 
 template <int B, int KC, int R, int EPI>

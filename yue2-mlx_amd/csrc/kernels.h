@@ -33,7 +33,6 @@ struct GemvParams {
   int epilogue = kEpiStore;
   int seg0_start = 0, seg0_len = 1 << 30, seg1_start = 0;  // row map
   int32_t *advance = nullptr;  // block 0 increments advance[0..batch)
-  int32_t *epoch = nullptr;    // block 0 increments *epoch (the step counter)
   // [batch][k] scratch for the batched (MFMA) form: with a gather or an
   // RMSNorm prologue, a row kernel first writes the prepared rows here once
   // instead of every workgroup re-normalising them.
@@ -98,41 +97,8 @@ struct AttnDecodeParams {
   int out_stride = 0;
 };
 hipError_t launch_attn_decode(const AttnDecodeParams &p, hipStream_t s);
-
-// One decode layer's QKV projection, attention and o_proj + residual in one
-// launch for 1-2 branches (fused.hip). q: the QKV GEMV (input RMSNorm, the
-// embedding gather in the first layer; y_stride = the q|k|v row width; its
-// y is unused). a: the attention (its qkv / out pointers are unused). o: the
-// o_proj GEMV with the residual epilogue into o.y = x; in the first layer
-// o.embed / o.tokens / o.embed_rows name the embedding rows that are x.
-// q/k/v and the attention output travel as activation words (per-layer
-// buffers [batch][q.y_stride] and [batch][o.x_stride]) tagged from *epoch.
-struct FusedLayerParams {
-  GemvParams q;
-  AttnDecodeParams a;
-  GemvParams o;
-  uint32_t *qkv_words = nullptr;
-  uint32_t *attn_words = nullptr;
-  // tagged attention split partials, [batch][kv_heads][max_splits] x
-  // (G * 64 + G) 16-byte vectors (G = heads / kv_heads); shared by all layers
-  u32x4 *part = nullptr;
-  int layer = 0;                   // tags the partials together with *epoch
-  const int32_t *epoch = nullptr;  // step counter advanced by the lm_head
-  int32_t *err = nullptr;          // sticky: a wait expired
-  long long max_ticks = 0;         // bound of one wait (100 MHz ticks)
-  int o_late = 0;                  // o_proj streams its weights only once its inputs are fresh
-  // optional profiling trace [workgroup][16] of the 100 MHz clock: start,
-  // inputs ready (0 for the QKV role), end, role (0 QKV, 1 attention,
-  // 2 o_proj) | XCC id << 8 | HW_ID << 32; attention only: [4] prologue
-  // done, [5] merge done (split 0), [6] split done, [7] partials stored,
-  // [8] merge inputs fresh (split 0), [9] prologue start
-  unsigned long long *trace = nullptr;
-  // set by launch_fused_layer
-  int qkv_blocks = 0, attn_blocks = 0, o_blocks = 0;
-  float scale = 0.f;
-};
-bool fused_layer_supported(int hidden, int heads, int kv_heads, int head_dim, int batch);
-hipError_t launch_fused_layer(FusedLayerParams p, hipStream_t s);
+// Splits per (branch, kv head) for a session (max_splits above).
+int attn_decode_splits(int batch, int kv_heads, int kv_stride);
 
 // Acoustic-model attention (nar_attention.hip, nar_attention.cpp:63-270):
 // q [batch][heads][q_len][128], k / v [batch][kv_heads][kv_len][128], out

@@ -99,10 +99,6 @@ _SIGS = {
     "yuear_session_write_logits": (C.c_int, [C.c_void_p, u16p, _P(C.c_void_p)]),
     "yuear_session_set_position": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, _P(C.c_void_p)]),
     "yuear_session_layer_step": (C.c_int, [C.c_void_p, C.c_int32, u16p, u16p, _P(C.c_void_p)]),
-    "yuear_session_set_decode_path": (C.c_int, [C.c_void_p, C.c_int32, _P(C.c_void_p)]),
-    "yuear_session_decode_path": (C.c_int32, [C.c_void_p]),
-    "yuear_session_trace_step": (C.c_int, [C.c_void_p, _P(C.c_uint64), C.c_int64,
-                                           _P(C.c_int32), _P(C.c_void_p)]),
     "yuear_session_time_steps": (C.c_int, [C.c_void_p, C.c_int32, _P(C.c_double),
                                            _P(C.c_void_p)]),
     "yuear_session_time_generate": (C.c_int, [C.c_void_p, _P(SamplingC), C.c_uint64, C.c_int32,
@@ -139,7 +135,6 @@ for _name, (_res, _args) in _SIGS.items():
     _fn.restype, _fn.argtypes = _res, _args
 
 EXPORTS = tuple(_SIGS)
-DECODE_PATHS = ("kernels", "persistent", "fused")  # YUEAR_DECODE_KERNELS, _PERSISTENT, _FUSED
 
 
 def _take_error(err):
@@ -549,29 +544,6 @@ class Session:
     def set_position(self, branch, position):
         err = C.c_void_p()
         _check(lib.yuear_session_set_position(self._h(), branch, position, C.byref(err)), err)
-
-    @property
-    def decode_path(self):
-        """"kernels" (one kernel per op) or "persistent" (one launch per step)."""
-        return DECODE_PATHS[lib.yuear_session_decode_path(self._h())]
-
-    @decode_path.setter
-    def decode_path(self, name):
-        err = C.c_void_p()
-        _check(lib.yuear_session_set_decode_path(self._h(), DECODE_PATHS.index(name),
-                                                 C.byref(err)), err)
-
-    def trace_step(self):
-        """Phase trace of one persistent decode step (positions restored):
-        uint64 [layers * 6 + 1][grid][2] of 100 MHz (ready, done) stamps."""
-        layers = self.engine.config["num_hidden_layers"]
-        cap = (layers * 6 + 1) * 4096 * 2
-        buf = np.zeros(cap, dtype=np.uint64)
-        grid = C.c_int32()
-        err = C.c_void_p()
-        _check(lib.yuear_session_trace_step(self._h(), buf.ctypes.data_as(_P(C.c_uint64)), cap,
-                                            C.byref(grid), C.byref(err)), err)
-        return buf[:(layers * 6 + 1) * grid.value * 2].reshape(layers * 6 + 1, grid.value, 2)
 
     def layer_step(self, layer, x):
         x = np.ascontiguousarray(x, dtype=np.uint16).reshape(self.branches, -1)
