@@ -28,7 +28,7 @@ constexpr int kAttnMaxSplits = 64;
 template <int G, int W>
 struct AttnShared {
   attn::Lds<G, W> sh;
-  float s_w[kAttnMaxSplits][G];  // merge weights
+  alignas(16) float s_w[G][kAttnMaxSplits];  // merge weights per head, 0 past the active splits
   int is_last;
 };
 
@@ -53,7 +53,9 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
   constexpr int kHeadsPerWave = (G + 2 + W - 1) / W;  // prologue heads (q heads, k, v)
   attn::Lds<G, W> &sh = sm.sh;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index is uniform: as a scalar, the per-wave head choice below
+  // selects kernel arguments instead of loading them through a vector address
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   constexpr int D = attn::D;
   const int Hkv = p.kv_heads;
   const int b = bh / Hkv, kvh = bh % Hkv;
@@ -146,7 +148,7 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
   wait_vmem();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED,
+    const int prev = __hip_atomic_fetch_add(&p.counters[bh * kCounterStride], 1, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
     sm.is_last = prev == nsplit - 1;
   }
@@ -154,13 +156,15 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
   if (!sm.is_last)
     return;
   const int n_active = (L + chunk - 1) / chunk;
-  // One memory round: the (m, l) of all splits first (wave w: heads w + W j,
-  // lane t: split t), then thread x's 8-byte partials of outputs (2 q,
-  // 2 q + 1), q = x + NT r, for up to kRound splits (clamped to the active
-  // ones); the merge weights are formed while the partials arrive.
+  // One memory round: the (m, l) of all splits (wave w: heads w + W j, lane
+  // t: split t) and thread x's 8-byte partials of outputs (2 q, 2 q + 1),
+  // q = x + NT r, of every active split; the merge weights are formed while
+  // the partials arrive and go to LDS per head ([G][splits], zero past the
+  // active splits), so the weighted sum reads them four at a time and runs
+  // without branches (adding 0 * 0 leaves the sum unchanged).
   constexpr int kPairs = G * D / 2;
   constexpr int kRounds = (kPairs + NT - 1) / NT;
-  constexpr int kRound = 32;
+  constexpr int kRound = kAttnMaxSplits;
   constexpr int kMergeHeads = (G + W - 1) / W;
   const auto rml = part_rsrc(p.part_ml + part * G * 2, uint32_t(n_active * G * 2) * 4);
   const auto ro = part_rsrc(p.part_o + part * (G * D), uint32_t(n_active * G * D) * 4);
@@ -176,15 +180,14 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
     unsigned long long ov[kRound];
 #pragma unroll
     for (int j = 0; j < kRound; ++j)
-      ov[j] = part_load2(ro, uint32_t(min(j, n_active - 1) * (G * D) + 2 * q) * 4);
+      ov[j] = j < n_active ? part_load2(ro, uint32_t(j * (G * D) + 2 * q) * 4) : 0ull;
     if (r == 0) {
 #pragma unroll
       for (int j = 0; j < kMergeHeads; ++j) {
         const int h = wave + W * j;
         if (h < G) {
           const float w = merge_weight(mm[j], ll[j], lane < n_active);
-          if (lane < n_active)
-            sm.s_w[lane][h] = w;
+          sm.s_w[h][lane] = lane < n_active ? w : 0.f;
         }
       }
       __syncthreads();
@@ -193,26 +196,24 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
       const int h = (2 * q) / D;
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-      for (int j = 0; j < kRound; ++j) {
-        if (j < n_active) {  // sequential over splits
-          const float o0 = __builtin_bit_cast(float, uint32_t(ov[j]));
-          const float o1 = __builtin_bit_cast(float, uint32_t(ov[j] >> 32));
-          a0 = fmaf(sm.s_w[j][h], o0, a0);
-          a1 = fmaf(sm.s_w[j][h], o1, a1);
+      for (int j4 = 0; j4 < kRound / 4; ++j4) {
+        if (4 * j4 >= n_active)  // uniform: the rest adds 0 * 0
+          break;
+        const float4 w4 = reinterpret_cast<const float4 *>(&sm.s_w[h][0])[j4];
+        const float wj[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {  // sequential over splits
+          const unsigned long long v = ov[4 * j4 + t];
+          a0 = fmaf(wj[t], __builtin_bit_cast(float, uint32_t(v)), a0);
+          a1 = fmaf(wj[t], __builtin_bit_cast(float, uint32_t(v >> 32)), a1);
         }
-      }
-      for (int j = kRound; j < n_active; ++j) {  // more splits than one round
-        const unsigned long long v =
-            part_load2(ro, uint32_t(j * (G * D) + 2 * q) * 4);
-        a0 = fmaf(sm.s_w[j][h], __builtin_bit_cast(float, uint32_t(v)), a0);
-        a1 = fmaf(sm.s_w[j][h], __builtin_bit_cast(float, uint32_t(v >> 32)), a1);
       }
       reinterpret_cast<uint32_t *>(p.out + size_t(b) * p.out_stride + size_t(kvh * G) * D)[q] =
           uint32_t(f2bf(a0)) | (uint32_t(f2bf(a1)) << 16);
     }
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&p.counters[bh * kCounterStride], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace yuear

@@ -154,6 +154,19 @@ __device__ __forceinline__ void pass(const Lds<G, W> &sh, const u32x4 *kc, const
     for (int dt = 0; dt < 8; ++dt)
       vr[dt] = with_elem(vr[dt], ep, vn[16 * dt + i]);
   }
+  // Values of keys at or past s1 are zeroed: their P is exactly 0, but a slot
+  // never written (or rewound) must not bring an Inf or NaN into P.V.
+  if (blk0 + kBlock > s1) {  // wave-uniform
+    const int nv = min(max(s1 - (blk0 + 8 * r), 0), 8);
+    uint32_t keep[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      keep[w] = (nv > 2 * w ? 0x0000ffffu : 0u) | (nv > 2 * w + 1 ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      vr[dt] = u32x4{vr[dt].x & keep[0], vr[dt].y & keep[1], vr[dt].z & keep[2],
+                     vr[dt].w & keep[3]};
+  }
   // scores of keys blk0 + 8 r + e, e = 4 T + t
   float sc[8];
 #pragma unroll

@@ -633,8 +633,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   const int G = c.Hq / c.Hkv;
   S.part_o = S.alloc<float>(size_t(branches) * c.Hkv * S.max_splits * G * c.D);
   S.part_ml = S.alloc<float>(size_t(branches) * c.Hkv * S.max_splits * G * 2);
-  S.counters = S.alloc<int32_t>(size_t(branches) * c.Hkv);
-  HIPC(hipMemsetAsync(S.counters, 0, size_t(branches) * c.Hkv * 4, S.stream));
+  S.counters = S.alloc<int32_t>(size_t(branches) * c.Hkv * kCounterStride);
+  HIPC(hipMemsetAsync(S.counters, 0, size_t(branches) * c.Hkv * kCounterStride * 4, S.stream));
   int pow2 = 1;
   while (pow2 < S.phase.size) pow2 <<= 1;
   // sampler buffers: one set per branch when more than two branches sample
@@ -1782,7 +1782,7 @@ int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
   static OpPool pool;
   void *buf = nullptr;
   bool fresh = false;
-  const size_t counter_bytes = 64 * 8 * 4;
+  const size_t counter_bytes = size_t(64) * 8 * kCounterStride * 4;
   hipError_t e = pool.get(static_cast<hipStream_t>(stream), counter_bytes + need * 4, &buf, &fresh);
   if (e != hipSuccess)
     return int32_t(e);

@@ -77,6 +77,11 @@ hipError_t launch_tile_rows(const uint16_t *w, int n, int k, uint16_t *out, hipS
 // 32): K row-major [capacity][128]; V in 32-slot blocks stored dim-major,
 // element (t, d) at attn::v_index(t, d) = (t / 32) * 4096 + d * 32 + t % 32.
 
+// Arrival counters of the decode attention sit kCounterStride ints (256
+// bytes) apart: the atomics of different (branch, kv head) pairs then land on
+// different memory channels instead of queueing on one cache line.
+constexpr int kCounterStride = 64;
+
 // Split-K flash-decode attention for one layer, all branches, with the
 // q/k RMSNorm + RoPE prologue, the KV append of the current token and the
 // last-block merge of the split partials fused in.
@@ -92,7 +97,7 @@ struct AttnDecodeParams {
   int max_splits = 1;
   float *part_o = nullptr;   // [batch][Hkv][max_splits][G][D]
   float *part_ml = nullptr;  // [batch][Hkv][max_splits][G][2]
-  int32_t *counters = nullptr;  // [batch][Hkv], zero between launches
+  int32_t *counters = nullptr;  // [batch][Hkv] x kCounterStride ints, zero between launches
   uint16_t *out = nullptr;      // [batch][out_stride]
   int out_stride = 0;
 };
