@@ -245,6 +245,24 @@ int32_t yuear_op_attention_decode(
     const uint16_t *dev_rope_sin, uint16_t *dev_k_cache, uint16_t *dev_v_cache,
     const int32_t *dev_pos, int32_t heads, int32_t kv_heads, int32_t capacity,
     int32_t batch, int32_t max_splits, uint16_t *dev_out, void *stream);
+/* yuear_op_attention_decode without any allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * split partials and arrival counters live in a fixed 4 MiB device array per
+ * GPU (YUEAR_NOALLOC_SCRATCH_BYTES), held until the process ends; a call
+ * whose layout needs more -- 128 KiB of counters plus
+ * batch * kv_heads * max_splits * (heads / kv_heads) * 130 floats -- returns
+ * hipErrorOutOfMemory (2) and launches nothing. The first call on a device
+ * looks up the array's address and clears its counters on `stream`. Calls
+ * on one GPU share the array: calls that overlap in time on one GPU race.
+ * Same arguments, kernels and results as yuear_op_attention_decode. */
+#define YUEAR_NOALLOC_SCRATCH_BYTES (4 << 20)
+int32_t yuear_op_attention_decode_noalloc(
+    const uint16_t *dev_qkv, const uint16_t *dev_q_norm,
+    const uint16_t *dev_k_norm, float eps, const uint16_t *dev_rope_cos,
+    const uint16_t *dev_rope_sin, uint16_t *dev_k_cache, uint16_t *dev_v_cache,
+    const int32_t *dev_pos, int32_t heads, int32_t kv_heads, int32_t capacity,
+    int32_t batch, int32_t max_splits, uint16_t *dev_out, void *stream);
 /* Affine group-64 quantized form of yuear_op_gemv for batch 1-2
  * (mx::quantized_matmul, ar.cpp:22-24): codes [n][k * bits / 32] uint32,
  * groups [n][k / 64] uint32 words scale | bias << 16 (bf16 halves). */

@@ -5,7 +5,10 @@
 // attn_block.h. The chunk length is derived on device from pos[b], so one
 // captured graph serves every KV length up to capacity.
 #include <cmath>
+#include <map>
+#include <mutex>
 
+#include "../../include/yuear.h"
 #include "attn_block.h"
 #include "common.h"
 #include "kernels.h"
@@ -62,3 +65,109 @@ int attn_decode_splits(int batch, int kv_heads, int kv_stride) {
 }
 
 }  // namespace yuear
+
+// ---------------------------------------------------------------------------
+// yuear_op_attention_decode_noalloc: the decode attention with its scratch in
+// a fixed device array instead of library-allocated memory.
+//
+// `scratch` holds the arrival counters (kNoallocCounterBytes: 512 (branch,
+// kv head) pairs, kCounterStride ints apart) and then the split partials. In
+// host code the array's name is only a stand-in: its device address, which
+// differs per GPU, is looked up once per device with hipGetSymbolAddress and
+// used for every kernel argument. Calls on one GPU share the array: calls
+// that overlap in time on one GPU race. The counters are cleared by a fill
+// kernel the first time a device is used (the attention's merging workgroup
+// returns each counter to zero after every launch).
+namespace yuear {
+namespace {
+
+constexpr size_t kNoallocBytes = size_t(4) << 20;
+constexpr size_t kNoallocCounterBytes = size_t(512) * kCounterStride * 4;
+static __device__ __align__(256) uint8_t scratch[kNoallocBytes];
+
+__global__ void zero_words_kernel(uint32_t *p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+struct NoallocScratch {
+  std::mutex mu;
+  std::map<int, uint8_t *> ptr;  // device -> address of `scratch` on it
+};
+NoallocScratch &noalloc_scratch() {
+  static NoallocScratch s;
+  return s;
+}
+
+// Address of this device's `scratch`; set up (symbol lookup, counters
+// cleared on `stream`) on the first call for the device.
+hipError_t noalloc_base(hipStream_t stream, uint8_t **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return e;
+  NoallocScratch &s = noalloc_scratch();
+  std::lock_guard<std::mutex> lock(s.mu);
+  auto it = s.ptr.find(dev);
+  if (it != s.ptr.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  void *p = nullptr;
+  if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess)
+    return e;
+  hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, stream,
+                     static_cast<uint32_t *>(p), int(kNoallocCounterBytes / 4));
+  if ((e = hipGetLastError()) != hipSuccess)
+    return e;
+  s.ptr[dev] = static_cast<uint8_t *>(p);
+  *out = static_cast<uint8_t *>(p);
+  return hipSuccess;
+}
+
+}  // namespace
+
+}  // namespace yuear
+
+extern "C" int32_t yuear_op_attention_decode_noalloc(
+    const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm, float eps,
+    const uint16_t *rope_cos, const uint16_t *rope_sin, uint16_t *k_cache, uint16_t *v_cache,
+    const int32_t *pos, int32_t heads, int32_t kv_heads, int32_t capacity, int32_t batch,
+    int32_t max_splits, uint16_t *out, void *stream) {
+  using namespace yuear;
+  if (batch < 1 || kv_heads < 1 || heads < kv_heads || heads % kv_heads || max_splits < 1 ||
+      size_t(batch) * kv_heads > 512)
+    return int32_t(hipErrorInvalidValue);
+  const int G = heads / kv_heads;
+  const size_t part_floats = size_t(batch) * kv_heads * max_splits * G * (128 + 2);
+  if (kNoallocCounterBytes + part_floats * 4 > kNoallocBytes)
+    return int32_t(hipErrorOutOfMemory);  // beyond the fixed scratch
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t *base = nullptr;
+  hipError_t e = noalloc_base(st, &base);
+  if (e != hipSuccess)
+    return int32_t(e);
+  AttnDecodeParams p;
+  p.qkv = qkv;
+  p.qkv_stride = (heads + 2 * kv_heads) * 128;
+  p.q_norm = q_norm;
+  p.k_norm = k_norm;
+  p.eps = eps;
+  p.rope_cos = rope_cos;
+  p.rope_sin = rope_sin;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.pos = pos;
+  p.heads = heads;
+  p.kv_heads = kv_heads;
+  p.head_dim = 128;
+  p.capacity = capacity;
+  p.batch = batch;
+  p.max_splits = max_splits;
+  p.counters = reinterpret_cast<int32_t *>(base);
+  p.part_o = reinterpret_cast<float *>(base + kNoallocCounterBytes);
+  p.part_ml = p.part_o + size_t(batch) * kv_heads * max_splits * G * 128;
+  p.out = out;
+  p.out_stride = heads * 128;
+  return int32_t(launch_attn_decode(p, st));
+}

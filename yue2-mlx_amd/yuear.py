@@ -112,6 +112,11 @@ _SIGS = {
                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                               C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                               C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
+    "yuear_op_attention_decode_noalloc": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p,
+                                                      C.c_float, C.c_void_p, C.c_void_p,
+                                                      C.c_void_p, C.c_void_p, C.c_void_p,
+                                                      C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                                      C.c_int32, C.c_void_p, C.c_void_p]),
     "yuear_op_qgemv": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_float,
                                    C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
