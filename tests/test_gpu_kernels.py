@@ -108,6 +108,7 @@ def prep_qk(oracle, raw, gain, pos, theta=5e5):
     (24, 8, [63], 64), (24, 8, [200], 64), (24, 8, [511], 64), (24, 8, [4095], 64),
     (24, 8, [4095], 1), (24, 8, [777], 7), (16, 8, [300], 32), (4, 2, [50], 8),
     (24, 8, [513, 1535], 32), (24, 8, [100, 1200, 7, 2047, 64, 500, 9, 1000], 32),
+    (24, 8, [8191], 64),  # KV 8192: one launch of the long-context decode
 ])
 def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_heads, batch_pos,
                                          splits):
@@ -257,7 +258,10 @@ def test_op_scratch_is_per_stream(torch, yuear_lib):
                                                    (65, 10, 24, 8), (200, 333, 16, 8),
                                                    # 24 x 33 = 792 workgroups of 64 queries:
                                                    # the LDS-shared tile, ragged last tile
-                                                   (2100, 40, 24, 8)])
+                                                   (2100, 40, 24, 8),
+                                                   # the 3000-token prefill, one pass and
+                                                   # its last chunk after 2048 cached keys
+                                                   (3000, 0, 24, 8), (952, 2048, 24, 8)])
 def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, heads, kv_heads):
     rng = np.random.default_rng(T + pos0)
     cap = yuear_lib.kv_slots(pos0 + T + 3)
