@@ -223,11 +223,11 @@ yuear_status yuear_session_time_kernel(yuear_session *session,
 
 /* ---- op-level entry points (model_ops, ar.hpp:8-19), device pointers,
  * `stream` is a hipStream_t (NULL = default stream). Scratch memory (the
- * batched GEMV's staging rows, the decode attention's split partials, the
- * GEMM's residual matrix and library workspace) is per (device, stream):
- * calls on different streams never share it. The first call on a stream (or
- * one needing a larger buffer) allocates, so make it outside graph capture;
- * yuear_op_gemm allocates stream-ordered (hipMallocAsync) on every call. ---- */
+ * batched GEMV's staging rows, the decode attention's split partials and
+ * arrival counters) is per (device, stream): calls on different streams
+ * never share it. The first call on a stream (or one needing a larger
+ * buffer) allocates, so make it outside graph capture; yuear_op_gemm uses
+ * no scratch. ---- */
 /* y[b][r] = bf16(x[b] . W[row(r)]) with optional RMSNorm prologue
  * (norm_w != NULL) and epilogue 0 store / 1 residual add / 2 SwiGLU pairs. */
 int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,
@@ -275,7 +275,9 @@ int32_t yuear_op_dequantize(const uint32_t *dev_codes, const uint32_t *dev_group
                             int32_t bits, int32_t n, int32_t k, uint16_t *dev_out,
                             void *stream);
 /* C[m][n] = bf16(A[m] . W[n]), or C = bf16(C + bf16(A[m] . W[n])) when
- * residual (the prefill projections, on hipBLASLt). */
+ * residual (the prefill projections, mx::matmul in ar.cpp:258-298), fp32
+ * accumulation on MFMA. k a multiple of 64, lda a multiple of 8, lda >= k,
+ * ldc >= n; otherwise hipErrorInvalidValue (1) and nothing is launched. */
 int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                       int32_t ldc, int32_t residual, void *stream);

@@ -200,11 +200,36 @@ def test_gemm_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual):
     assert_close_bf16(host(torch, dc), ref, scale=scale, exact_frac=0.9)
 
 
+@pytest.mark.parametrize("m,n,k,residual", [
+    (3000, 5120, 3072, 0), (3000, 3072, 3072, 1), (3000, 16384, 3072, 0), (3000, 3072, 8192, 1),
+    (4096, 16384, 3072, 0), (2049, 3072, 8192, 1),
+])
+def test_gemm_prefill_shapes(torch, yuear_lib, oracle, m, n, k, residual):
+    """The four projections of a prefill (QKV, output, gate/up, down) at
+    3000, 4096 and 2049 tokens (large enough for the 256 x 256 tile on a
+    256-CU part, and a ragged last tile row): 96 rows, among them the first
+    and last of every 256-row tile, against the oracle."""
+    rng = np.random.default_rng(m + n + k)
+    a = bf(rng.normal(size=(m, k)))
+    w = bf(rng.normal(size=(n, k)) * 0.02)
+    c0 = bf(rng.normal(size=(m, n))) if residual else np.zeros((m, n), np.uint16)
+    da, dw, dc = dev(torch, a), dev(torch, w), dev(torch, c0)
+    assert yuear_lib.lib.yuear_op_gemm(da.data_ptr(), k, dw.data_ptr(), m, n, k, dc.data_ptr(),
+                                       n, residual, None) == 0
+    got = host(torch, dc)
+    edges = [r for t in range(0, m, 256) for r in (t, min(t + 255, m - 1))]
+    rows = np.unique(np.concatenate([edges, rng.integers(0, m, size=96 - len(set(edges)))]))
+    acc = oracle.linear(a[rows], w)
+    ref = bf(f(c0[rows]) + f(acc)) if residual else acc
+    scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+    assert_close_bf16(got[rows], ref, scale=scale, exact_frac=0.9)
+
+
 def test_op_scratch_is_per_stream(torch, yuear_lib):
     """Residual GEMMs and decode attentions issued on two streams at once
-    equal the same calls made one at a time: the op-level scratch (residual
-    matrix, library workspace, split partials and counters) is never shared
-    between streams."""
+    equal the same calls made one at a time: the op-level scratch (split
+    partials and counters) is never shared between streams, and the GEMM
+    keeps nothing between calls."""
     rng = np.random.default_rng(31)
     m, n, k = 300, 3072, 3072
     heads, kv, pos, cap = 24, 8, 700, 736

@@ -276,7 +276,6 @@ struct yuear_session {
   int scratch_u_stride = 0;
   // prefill scratch
   int chunk = 0;
-  void *gemm_ws = nullptr;  // prefill GEMM workspace (kGemmWorkspace bytes)
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
            *pgu = nullptr, *pact = nullptr;
   int32_t *pids = nullptr;
@@ -654,7 +653,6 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   const size_t T = S.chunk;
   S.px = S.alloc<uint16_t>(T * c.H);
   S.ph = S.alloc<uint16_t>(T * c.H);
-  S.gemm_ws = S.alloc<uint8_t>(kGemmWorkspace);  // hipBLASLt scratch of this session's stream
   S.pqkv = S.alloc<uint16_t>(T * c.qkv());
   S.pq = S.alloc<uint16_t>(T * c.Hq * c.D);
   S.pattn = S.alloc<uint16_t>(T * c.Hq * c.D);
@@ -933,7 +931,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       const LayerW &L = E.layers[l];
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.input_ln, c.eps, S.ph, st));
       GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0};
-      HIPC(launch_gemm(g, nullptr, S.gemm_ws, kGemmWorkspace, st));
+      HIPC(launch_gemm(g, st));
       QkPrepParams qp;
       qp.qkv = S.pqkv;
       qp.qkv_stride = c.qkv();
@@ -965,13 +963,13 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       ap.out = S.pattn;
       HIPC(launch_attn_prefill(ap, st));
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
-      HIPC(launch_gemm(og, S.ph, S.gemm_ws, kGemmWorkspace, st));  // S.ph is free until the next RMSNorm
+      HIPC(launch_gemm(og, st));
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
       GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pgu, 2 * c.F, 0};
-      HIPC(launch_gemm(gu, nullptr, S.gemm_ws, kGemmWorkspace, st));
+      HIPC(launch_gemm(gu, st));
       HIPC(launch_swiglu_rows(S.pgu, T, c.F, S.pact, st));
       GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1};
-      HIPC(launch_gemm(dg, S.ph, S.gemm_ws, kGemmWorkspace, st));
+      HIPC(launch_gemm(dg, st));
     }
     S.host_pos[b] += T;
     if (start + T >= n)  // final norm + projection of the last hidden row
@@ -1819,27 +1817,7 @@ int32_t yuear_op_attention_decode(const uint16_t *qkv, const uint16_t *q_norm,
 int32_t yuear_op_gemm(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t m, int32_t n,
                       int32_t k, uint16_t *c, int32_t ldc, int32_t residual, void *stream) {
   GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
-  // stream-ordered scratch (the residual matrix, the library's workspace):
-  // calls on different streams or devices never share one
-  if (m < 1 || n < 1 || k < 1 || lda < k || ldc < n || !a || !w || !c)
-    return int32_t(hipErrorInvalidValue);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  size_t ws_bytes = 0;
-  hipError_t e = gemm_workspace_bytes(p, &ws_bytes);
-  if (e != hipSuccess)
-    return int32_t(e);
-  const size_t res_bytes = residual ? size_t(m) * ldc * 2 : 0;
-  uint8_t *buf = nullptr;
-  if (ws_bytes + res_bytes > 0) {
-    e = hipMallocAsync(reinterpret_cast<void **>(&buf), ws_bytes + res_bytes + 256, st);
-    if (e != hipSuccess)
-      return int32_t(e);
-  }
-  uint16_t *scratch = residual ? reinterpret_cast<uint16_t *>(buf) : nullptr;
-  void *ws = ws_bytes ? buf + (res_bytes + 255) / 256 * 256 : nullptr;
-  e = launch_gemm(p, scratch, ws, ws_bytes, st);
-  const hipError_t f = buf ? hipFreeAsync(buf, st) : hipSuccess;
-  return int32_t(e != hipSuccess ? e : f);
+  return int32_t(launch_gemm(p, static_cast<hipStream_t>(stream)));
 }
 
 int32_t yuear_op_attention_prefill(const uint16_t *q, const uint16_t *k_cache,

@@ -174,15 +174,8 @@ struct GemmParams {
   int ldc = 0;
   int residual = 0;             // c = bf16(c + bf16(acc))
 };
-// On hipBLASLt (blas.hip). The residual form needs `scratch`, a [m][ldc]
-// bf16 matrix that receives bf16(acc) before the add (n and ldc multiples
-// of 8). `workspace` (workspace_bytes, at most kGemmWorkspace are used) is
-// the library's scratch for this stream: never shared with a GEMM in flight
-// on another stream. gemm_workspace_bytes gives what p's algorithm needs.
-constexpr size_t kGemmWorkspace = size_t(64) << 20;
-hipError_t gemm_workspace_bytes(const GemmParams &p, size_t *bytes);
-hipError_t launch_gemm(const GemmParams &p, uint16_t *scratch, void *workspace,
-                       size_t workspace_bytes, hipStream_t s);
+// MFMA GEMM (gemm.hip); k a multiple of 64, lda a multiple of 8. No scratch.
+hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
                              int width, uint16_t *out, hipStream_t s);

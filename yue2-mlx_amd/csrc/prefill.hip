@@ -1,5 +1,5 @@
-// Prompt prefill kernels on gfx950 (the projections are GEMMs on hipBLASLt,
-// blas.hip): row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV
+// Prompt prefill kernels on gfx950 (the projections are MFMA GEMMs,
+// gemm.hip): row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV
 // append, and an MFMA causal attention with fp32 opmath.
 //
 // Reference: native/src/ar.cpp:246-301 (hidden() over T > 1 tokens) and
