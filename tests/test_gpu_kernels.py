@@ -225,6 +225,24 @@ def test_gemm_prefill_shapes(torch, yuear_lib, oracle, m, n, k, residual):
     assert_close_bf16(got[rows], ref, scale=scale, exact_frac=0.9)
 
 
+@pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])
+def test_gemm_split_k_is_deterministic(torch, yuear_lib, m, n, k):
+    """Shapes whose tiles fill less than a round of CUs split K over several
+    workgroups; the partials are summed in K order whichever workgroup
+    arrives last, so repeated launches give identical bits."""
+    rng = np.random.default_rng(m + 3 * n)
+    a = dev(torch, bf(rng.normal(size=(m, k))))
+    w = dev(torch, bf(rng.normal(size=(n, k)) * 0.02))
+    outs = []
+    for _ in range(3):
+        c = dev(torch, np.zeros((m, n), np.uint16))
+        assert yuear_lib.lib.yuear_op_gemm(a.data_ptr(), k, w.data_ptr(), m, n, k, c.data_ptr(),
+                                           n, 0, None) == 0
+        outs.append(host(torch, c))
+    for o in outs[1:]:
+        np.testing.assert_array_equal(outs[0], o)
+
+
 def test_op_scratch_is_per_stream(torch, yuear_lib):
     """Residual GEMMs and decode attentions issued on two streams at once
     equal the same calls made one at a time: the op-level scratch (split

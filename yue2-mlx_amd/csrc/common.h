@@ -219,10 +219,13 @@ __device__ __forceinline__ float merge_weight(float m, float l, bool active) {
 
 // Reinterpret one packed bf16 pair. The element must arrive by value: this
 // clang reads element 0 when __builtin_bit_cast is applied directly to an
-// ext_vector element lvalue such as v.y.
+// ext_vector element lvalue such as v.y or v[3] (the by-value helpers below
+// exist for that reason).
 __device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t v) {
   return __builtin_bit_cast(bf16x2_t, v);
 }
+__device__ __forceinline__ uint32_t f32_bits(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float bits_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
 // dot of 8 bf16 pairs packed in two u32x4 registers, fp32 accumulate.
 __device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
   acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a.x), as_bf16x2(b.x), acc, false);

@@ -3,21 +3,32 @@
 // with one rounding, or the residual form C = bf16(C + bf16(acc)) with both
 // of the reference's rounding points (native/src/ar.cpp:20-29, 292-298).
 //
-// Tiling: a workgroup owns a BM x BN tile of C and walks K in 64-wide steps.
-// Its WM x WN waves each own a (BM / WM) x (BN / WN) sub-tile of 32 x 32
-// v_mfma_f32_32x32x16_bf16 tiles (fp32 accumulators). Each K step's A and W
-// slabs (BM x 64 and BN x 64 bf16) are loaded from global memory with
-// 16-byte buffer loads (rows past M or N read as zero), parked in registers
-// while the previous step computes, then written to the other half of a
-// two-stage LDS ring (rows padded to 72 elements against bank conflicts):
-// one barrier per K step. MFMA operands are read from LDS as 16-byte
-// fragments: lane l holds row (l % 32), k 8 (l / 32) + [0, 8) of a 16-wide K
-// sub-step; the 32 x 32 result leaves lane l with column (l % 32), rows
-// 8 (r / 4) + 4 (l / 32) + r % 4 for its 16 values r.
+// Tiling: a workgroup of WM x WN waves computes a BM x BN tile of C; each
+// wave owns (BM / WM) token rows x (BN / WN) features as 32 x 32
+// v_mfma_f32_32x32x16_bf16 tiles (fp32 accumulators) with the weights as the
+// MFMA's first operand, so a lane ends up holding 4 consecutive features of
+// one token row (8-byte stores). K advances 64 at a time through a two-stage
+// LDS ring filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds):
+// each load instruction moves 8 rows x 128 bytes into one contiguous KiB
+// without passing through registers; the workgroup's (BM + BN) / 8 blocks per
+// step are spread evenly over its waves. Rows past M or N read as zero
+// (buffer range). One barrier per K step; the next step's loads are in flight
+// while the current one computes.
 //
-// Shapes: 256 x 256 tiles (8 waves, 147 KiB of LDS, one workgroup per CU)
-// when they give at least one tile per CU, else 128 x 128 tiles (4 waves,
-// 74 KiB, two per CU).
+// LDS stage: A rows [BM][128 B] then W rows [BN][128 B]. The 16-byte chunk
+// kc (k = 8 kc .. 8 kc + 7) of row R is stored at slot kc ^ f(R),
+// f(R) = (R & 7) ^ ((R >> 3) & 1), so the MFMA fragment reads (16 lanes on 16
+// consecutive rows, one chunk) hit 16 distinct 4-bank groups. Fragment of a
+// 16-wide K sub-step s: lane l reads row l % 32, chunk 2 s + l / 32.
+//
+// Tile shapes (launch_gemm picks the one with the least estimated time for
+// the shape and the CU count): 256 x 256 (8 waves of 128 x 64), 256 x 128 and
+// 128 x 256 (8 waves of 64 x 64), 256 x 192 (8 waves of 64 x 96) and
+// 128 x 128 (4 waves of 64 x 64, two workgroups per CU). At the 3B prefill
+// shapes (M = 3000) QKV and gate/up take 256 x 256 tiles, the output and down
+// projections (N = 3072, 144 such tiles for 256 CUs) 256 x 192.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -27,9 +38,15 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-constexpr int BK = 64;
-constexpr int LDSK = BK + 8;  // LDS row stride in elements (144 bytes)
+constexpr int kBK = 64;  // K per step; one LDS row = 128 bytes
+
+// The kernel's only LDS object (dynamic size: 2 stages of (BM + BN) rows).
+// With a second __shared__ variable the compiler no longer tells the
+// direct-to-LDS writes of one stage from the reads of the other and waits for
+// every load in flight (vmcnt(0)) before each step's first LDS read.
+extern __shared__ __attribute__((aligned(1024))) char gemm_lds[];
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void *base, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
@@ -37,50 +54,44 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void *base, si
                                            0x00020000);
 }
 
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmParams p) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // MFMA tiles per wave
-  constexpr int CPR = BK / 8;                          // 16-byte chunks per slab row
-  constexpr int ACH = BM * CPR / NT, BCH = BN * CPR / NT;
-  static_assert(ACH * NT == BM * CPR && BCH * NT == BN * CPR, "slab chunks per thread");
-  extern __shared__ uint16_t lds[];
-  // stage st: A slab at lds + st (BM + BN) LDSK, W slab BM LDSK after it
-  auto as = [&](int st) { return lds + st * (BM + BN) * LDSK; };
-  auto bs = [&](int st) { return lds + st * (BM + BN) * LDSK + BM * LDSK; };
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return uint32_t(f2bf(a)) | uint32_t(f2bf(b)) << 16;
+}
 
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32 x 32 MFMA tiles per wave
+  constexpr int ABLK = BM / 8, BLK = (BM + BN) / 8;   // 1 KiB load blocks per stage
+  constexpr int BPW = BLK / NW;                        // per wave
+  constexpr int STAGE = (BM + BN) * 128;
+  static_assert(TM * WM * 32 == BM && TN * WN * 32 == BN && BPW * NW == BLK, "tile shape");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const auto ra = rows_rsrc(p.a + size_t(m0) * p.lda, size_t(max(p.m - m0, 0)) * p.lda * 2);
-  const auto rw = rows_rsrc(p.w + size_t(n0) * p.k, size_t(max(p.n - n0, 0)) * p.k * 2);
+  const int h = lane >> 5;
+  const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
+  const auto ra = rows_rsrc(p.a + size_t(m0) * p.lda, size_t(p.m - m0) * p.lda * 2);
+  const auto rw = rows_rsrc(p.w + size_t(n0) * p.k, size_t(p.n - n0) * p.k * 2);
 
-  u32x4 sa[ACH], sb[BCH];
-  auto load = [&](int k0) {
+  // this wave's blocks q = wave BPW + i of the stage's A | W block list:
+  // lane l loads row 8 q' + l / 8, chunk (l % 8) ^ f(row), into LDS slot l % 8
+  uint32_t goff[BPW];
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + i * NT, row = c / CPR, kc = c % CPR;
-      sa[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          ra, uint32_t((size_t(row) * p.lda + k0 + kc * 8) * 2), 0, 0);
-    }
+  for (int i = 0; i < BPW; ++i) {
+    const int q = wave * BPW + i;
+    const bool is_a = q < ABLK;
+    const int row = 8 * (is_a ? q : q - ABLK) + (lane >> 3);
+    const int kc = (lane & 7) ^ (lane >> 3) ^ (q & 1);
+    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8) * 2;
+  }
+  auto dma = [&](int st, int k0) {
+    char *stage = gemm_lds + st * STAGE;
 #pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + i * NT, row = c / CPR, kc = c % CPR;
-      sb[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          rw, uint32_t((size_t(row) * p.k + k0 + kc * 8) * 2), 0, 0);
-    }
-  };
-  auto stash = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + i * NT;
-      *reinterpret_cast<u32x4 *>(as(st) + (c / CPR) * LDSK + (c % CPR) * 8) = sa[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + i * NT;
-      *reinterpret_cast<u32x4 *>(bs(st) + (c / CPR) * LDSK + (c % CPR) * 8) = sb[i];
+    for (int i = 0; i < BPW; ++i) {
+      const int q = wave * BPW + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q < ABLK ? ra : rw, (lds_ptr_t)(stage + q * 1024),
+                                               16, goff[i] + k0 * 2, 0, 0, 0);
     }
   };
 
@@ -93,86 +104,207 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(GemmParams p) {
       for (int r = 0; r < 16; ++r)
         acc[i][j][r] = 0.f;
 
-  const int steps = p.k / BK;
-  load(0);
-  stash(0);
-  __syncthreads();
-  const int frow = lane & 31, fk = 8 * (lane >> 5);
-  for (int kt = 0; kt < steps; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < steps)
-      load((kt + 1) * BK);
-    const uint16_t *a_s = as(st) + (wm * (BM / WM) + frow) * LDSK + fk;
-    const uint16_t *b_s = bs(st) + (wn * (BN / WN) + frow) * LDSK + fk;
+  // fragment addresses: row (l % 32) of the wave's slice, chunk (2 s + h) ^ f
+  const int f = (lane & 7) ^ ((lane >> 3) & 1);
+  const int a_row = (wm * (BM / WM) + (lane & 31)) * 128;
+  const int w_row = BM * 128 + (wn * (BN / WN) + (lane & 31)) * 128;
+  const int steps = p.k / kBK;
+  bf16x8_t af[2][TM], wf[2][TN];
+  // fragments of sub-step s of the stage at `stage`, W and A tiles in the
+  // order the MFMAs use them, so the first MFMA waits for two reads only
+  auto rd = [&](const char *stage, int buf, int s) {
+    const int co = ((2 * s + h) ^ f) * 16;
 #pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      bf16x8_t af[TM], bf[TN];
+    for (int x = 0; x < (TM > TN ? TM : TN); ++x) {
+      if (x < TN)
+        wf[buf][x] = *reinterpret_cast<const bf16x8_t *>(stage + w_row + x * 4096 + co);
+      if (x < TM)
+        af[buf][x] = *reinterpret_cast<const bf16x8_t *>(stage + a_row + x * 4096 + co);
+    }
+  };
+  auto mfma = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t *>(a_s + i * 32 * LDSK + s * 16);
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const bf16x8_t *>(b_s + j * 32 * LDSK + s * 16);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[buf][j], af[buf][i], acc[i][j],
+                                                            0, 0, 0);
+  };
+  // Step kt reads stage kt & 1. Its barrier sits before the last sub-step's
+  // MFMAs, whose fragments are already in registers: past it, every wave has
+  // finished reading stage kt & 1 (it is refilled with step kt + 2) and every
+  // wave's part of step kt + 1 has landed (the first fragments of step kt + 1
+  // are read), both under those MFMAs. Loads past K (the last two steps'
+  // refills) read zeros or other rows into a stage nobody reads again.
+  dma(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // (a barrier waits for no global load)
+  if (steps > 1)
+    dma(1, kBK);
+  __syncthreads();
+  rd(gemm_lds, 0, 0);
+  for (int kt = 0; kt < steps; ++kt) {
+    const char *stage = gemm_lds + (kt & 1) * STAGE;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    for (int s = 0; s + 1 < kBK / 16; ++s) {
+      rd(stage, (s + 1) & 1, s + 1);
+      mfma(s & 1);
     }
-    if (kt + 1 < steps)
-      stash(st ^ 1);
+    // each sub-step: the next sub-step's reads one per MFMA
+#pragma unroll
+    for (int s = 0; s + 1 < kBK / 16; ++s) {
+#pragma unroll
+      for (int q = 0; q < TM + TN; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of step kt + 1, its LDS reads
     __syncthreads();
+    dma(kt & 1, (kt + 2) * kBK);
+    rd(gemm_lds + ((kt + 1) & 1) * STAGE, 0, 0);  // stale past the last step, unused
+    mfma((kBK / 16 - 1) & 1);
+    // refill loads and next reads spread over the last sub-step's MFMAs
+#pragma unroll
+    for (int q = 0; q < TM * TN; ++q) {
+      if (q < BPW)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (q < TM + TN)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // refills past K still in flight
 
-  // epilogue: lane holds column (lane % 32), rows 8 (r / 4) + 4 (lane / 32) + r % 4
-  const int col = lane & 31, rsub = 4 * (lane >> 5);
+  // epilogue: lane holds token row i 32 + l % 32 of the wave's slice, and
+  // features j 32 + 8 q + 4 h + [0, 4) of its slice
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * (BM / WM) + i * 32 + (lane & 31);
+    if (m >= p.m)
+      continue;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * (BN / WN) + j * 32 + col;
-      if (n >= p.n)
-        continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-        if (m < p.m) {
-          uint16_t *c = p.c + size_t(m) * p.ldc + n;
-          const float v = acc[i][j][r];
-          *c = p.residual ? f2bf(bf2f(*c) + rbf(v)) : f2bf(v);
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * (BN / WN) + j * 32 + 8 * q + 4 * h;
+        uint16_t *c = p.c + size_t(m) * p.ldc + n;
+        const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]};
+        if (n + 3 < p.n && (p.ldc & 3) == 0) {
+          uint2 o;
+          if (p.residual) {
+            const uint2 old = *reinterpret_cast<const uint2 *>(c);
+            o.x = pack_bf16x2(bf2f(uint16_t(old.x)) + rbf(v[0]),
+                              bf2f(uint16_t(old.x >> 16)) + rbf(v[1]));
+            o.y = pack_bf16x2(bf2f(uint16_t(old.y)) + rbf(v[2]),
+                              bf2f(uint16_t(old.y >> 16)) + rbf(v[3]));
+          } else {
+            o.x = pack_bf16x2(v[0], v[1]);
+            o.y = pack_bf16x2(v[2], v[3]);
+          }
+          *reinterpret_cast<uint2 *>(c) = o;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.n)
+              c[e] = p.residual ? f2bf(bf2f(c[e]) + rbf(v[e])) : f2bf(v[e]);
         }
       }
     }
   }
 }
 
+// One kernel per tile shape. The kernels are not templates: this clang emits
+// no host launch stub for these kernel bodies when the kernel itself is a
+// template instantiated from host code.
+#define YUEAR_GEMM_KERNEL(NAME, BM, BN, WM, WN)                                  \
+  __global__ __launch_bounds__(WM * WN * 64) void NAME(GemmParams p, int tiles_n) { \
+    gemm_tile<BM, BN, WM, WN>(p, tiles_n);                                       \
+  }
+YUEAR_GEMM_KERNEL(gemm_256x256, 256, 256, 2, 4)
+YUEAR_GEMM_KERNEL(gemm_256x128, 256, 128, 4, 2)
+YUEAR_GEMM_KERNEL(gemm_128x256, 128, 256, 2, 4)
+YUEAR_GEMM_KERNEL(gemm_256x192, 256, 192, 4, 2)
+YUEAR_GEMM_KERNEL(gemm_128x128, 128, 128, 2, 2)
+#undef YUEAR_GEMM_KERNEL
+
+// Time model of the tile shapes, in microseconds per 48 K steps measured on
+// MI355X (K = 3072, 256 CUs): `alone` for a tile with a CU to itself on an
+// otherwise idle chip, `busy` with every CU holding one such tile, `round` for
+// a full round of per_cu workgroups on every CU.
+struct TileShape {
+  int bm, bn, per_cu;
+  double alone, busy, round;
+};
+constexpr TileShape kShapes[] = {
+    {256, 256, 1, 63.0, 85.0, 85.0}, {256, 128, 1, 43.5, 50.0, 50.0},
+    {128, 256, 1, 44.3, 50.0, 50.0}, {256, 192, 1, 50.5, 60.0, 60.0},
+    {128, 128, 2, 34.3, 40.0, 50.8},
+};
+
 template <int BM, int BN, int WM, int WN>
-hipError_t launch_tile(const GemmParams &p, hipStream_t s) {
-  auto kern = gemm_kernel<BM, BN, WM, WN>;
-  const size_t lds = size_t(2) * (BM + BN) * LDSK * 2;
+hipError_t launch_tile(void (*kern)(GemmParams, int), const GemmParams &p, hipStream_t s) {
+  const int lds = 2 * (BM + BN) * 128;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess)
     return e;
-  hipLaunchKernelGGL(kern, dim3((p.n + BN - 1) / BN, (p.m + BM - 1) / BM), dim3(WM * WN * 64),
-                     lds, s, p);
+  const int tiles_n = (p.n + BN - 1) / BN;
+  const unsigned tiles = unsigned((p.m + BM - 1) / BM) * unsigned(tiles_n);
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(WM * WN * 64), lds, s, p, tiles_n);
   return hipGetLastError();
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  return cus;
 }
 
 }  // namespace
 
-hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
-  if (p.m < 1 || p.n < 1 || p.k < BK || p.k % BK || p.lda < p.k || p.ldc < p.n || p.lda % 8 ||
-      !p.a || !p.w || !p.c)
+int gemm_tile_choice(int m, int n, int cus) {
+  int best = 0;
+  double best_t = 0;
+  for (int i = 0; i < int(sizeof(kShapes) / sizeof(kShapes[0])); ++i) {
+    const TileShape &t = kShapes[i];
+    const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const long long slots = (long long)cus * t.per_cu;
+    const long long full = tiles / slots, rem = tiles % slots;
+    // full rounds, then a last round that is cheaper the fewer CUs it loads
+    double time = double(full) * t.round;
+    if (rem > cus)
+      time += t.round;
+    else if (rem > 0)
+      time += t.alone + (t.busy - t.alone) * double(rem) / cus;
+    if (i == 0 || time < best_t * 0.999) {
+      best = i;
+      best_t = time;
+    }
+  }
+  return best;
+}
+
+hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s) {
+  if (p.m < 1 || p.n < 1 || p.k < kBK || p.k % kBK || p.lda < p.k || p.ldc < p.n ||
+      p.lda % 8 || !p.a || !p.w || !p.c)
     return hipErrorInvalidValue;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
-  const long tiles256 = long((p.m + 255) / 256) * ((p.n + 255) / 256);
-  if (tiles256 >= cus)
-    return launch_tile<256, 256, 2, 4>(p, s);
-  return launch_tile<128, 128, 2, 2>(p, s);
+  switch (shape) {
+  case 0: return launch_tile<256, 256, 2, 4>(gemm_256x256, p, s);
+  case 1: return launch_tile<256, 128, 4, 2>(gemm_256x128, p, s);
+  case 2: return launch_tile<128, 256, 2, 4>(gemm_128x256, p, s);
+  case 3: return launch_tile<256, 192, 4, 2>(gemm_256x192, p, s);
+  case 4: return launch_tile<128, 128, 2, 2>(gemm_128x128, p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
+  return launch_gemm_tile(p, gemm_tile_choice(p.m, p.n, device_cus()), s);
 }
 
 }  // namespace yuear
