@@ -93,3 +93,37 @@ def test_sampling_struct_defaults_follow_reference(yuear_lib):
     s = yuear_lib.sampling_struct(None)  # types.hpp:29-33
     assert (s.temperature, s.top_p, s.top_k, s.repetition_penalty, s.penalty_window,
             s.min_tokens, s.max_tokens) == (1.0, 0.95, 100, 1.2, 50, 200, 9000)
+
+
+def test_cxx_facade_compiles_and_links(tmp_path):
+    """include/yuear.hpp (the C++20 facade with the reference's
+    generate_tokens signature) and its driver build against libyuear.so."""
+    out = tmp_path / "facade"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror",
+                    "-I" + os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "cxx", "facade_test.cpp"), "-o", str(out),
+                    "-L" + os.path.dirname(LIB), "-lyuear"], check=True)
+    assert out.exists()
+
+
+def test_cxx_facade_error_json_parser():
+    """yuear::detail::json_string against the library's error JSON form."""
+    src = r'''
+#include "yuear.hpp"
+#include <cstdio>
+int main() {
+  const std::string j = "{\"type\":\"ValueError\",\"message\":\"top_p must be in (0, 1] \\\"x\\\"\\n\"}";
+  std::printf("%s|%s|", yuear::detail::json_string(j, "type").c_str(),
+              yuear::detail::json_string(j, "message").c_str());
+  std::printf("%d", int(yuear::detail::json_string(j, "missing").empty()));
+}
+'''
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        cpp, exe = os.path.join(d, "t.cpp"), os.path.join(d, "t")
+        open(cpp, "w").write(src)
+        subprocess.run(["g++", "-std=c++20", "-I" + os.path.join(ROOT, "include"), cpp, "-o", exe,
+                        "-L" + os.path.dirname(LIB), "-lyuear",
+                        "-Wl,-rpath," + os.path.dirname(LIB)], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    assert out == 'ValueError|top_p must be in (0, 1] "x"\n|1'
