@@ -17,6 +17,8 @@
 //     desc, index asc), portable-exp softmax and the shifted-cumsum cut
 //     evaluated sequentially in that order; Gumbel-max draw with Philox
 //     uniforms u(seed, step, index).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -272,49 +274,68 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
 
   int local = 0;
   if (greedy) {  // sampling.cpp:247: argmax, lowest index on ties
-    float bv = ninf;
-    int bi = 0x7fffffff;
-    int c_from = tid;
-    if (prefetch) {
+    // Scan of this thread's logits; with kCheck the special rows (an LDS
+    // bitmap) are skipped. The special rows are few, so the first scan takes
+    // every row's plain score without the per-element bitmap look-up: when
+    // its winner is not special it is the best of the non-special rows, and
+    // only the penalised rows (rescored below) can still beat it. A special
+    // winner falls back to the checked scan.
+    auto scan = [&](auto check_tag, float &bv, int &bi) {
+      constexpr bool kCheck = decltype(check_tag)::value;
+      bv = ninf;
+      bi = 0x7fffffff;
+      int c_from = tid;
+      if (prefetch) {
 #pragma unroll
-      for (int u = 0; u < kPre; ++u) {
-        const int c = tid + u * kT;
-        if (c >= n8)
-          break;
-        const uint32_t w[4] = {pre[u].x, pre[u].y, pre[u].z, pre[u].w};
+        for (int u = 0; u < kPre; ++u) {
+          const int c = tid + u * kT;
+          if (c >= n8)
+            break;
+          const uint32_t w[4] = {pre[u].x, pre[u].y, pre[u].z, pre[u].w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float v = e & 1 ? bfhi(w[e >> 1]) : bflo(w[e >> 1]);
-          if (!special(sh, 8 * c + e) && better(v, 8 * c + e, bv, bi)) {
-            bv = v;
-            bi = 8 * c + e;
+          for (int e = 0; e < 8; ++e) {
+            const float v = e & 1 ? bfhi(w[e >> 1]) : bflo(w[e >> 1]);
+            if ((!kCheck || !special(sh, 8 * c + e)) && better(v, 8 * c + e, bv, bi)) {
+              bv = v;
+              bi = 8 * c + e;
+            }
           }
         }
+        c_from = tid + kPre * kT;
       }
-      c_from = tid + kPre * kT;
-    }
-    for (int c0 = c_from; c0 < n8; c0 += 2 * kT) {
-      float v[2][8];
-      const int c1 = min(c0 + kT, n8 - 1);
-      cx.chunk(c0, v[0]);
-      cx.chunk(c1, v[1]);
+      for (int c0 = c_from; c0 < n8; c0 += 2 * kT) {
+        float v[2][8];
+        const int c1 = min(c0 + kT, n8 - 1);
+        cx.chunk(c0, v[0]);
+        cx.chunk(c1, v[1]);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (h == 1 && c0 + kT >= n8) break;
-        const int base = 8 * (h ? c1 : c0);
+        for (int h = 0; h < 2; ++h) {
+          if (h == 1 && c0 + kT >= n8) break;
+          const int base = 8 * (h ? c1 : c0);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (!special(sh, base + e) && better(v[h][e], base + e, bv, bi)) {
-            bv = v[h][e];
-            bi = base + e;
-          }
+          for (int e = 0; e < 8; ++e)
+            if ((!kCheck || !special(sh, base + e)) && better(v[h][e], base + e, bv, bi)) {
+              bv = v[h][e];
+              bi = base + e;
+            }
+        }
       }
+      for (int i = 8 * n8 + tid; i < n; i += kT)
+        if ((!kCheck || !special(sh, i)) && better(cx.one(i), i, bv, bi)) {
+          bv = cx.one(i);
+          bi = i;
+        }
+    };
+    float bv, rv;
+    int bi, raw;
+    scan(std::integral_constant<bool, false>{}, bv, bi);
+    block_argmax(bv, bi, sh, &rv, &raw);
+    if (raw != 0x7fffffff && special(sh, raw)) {  // uniform: every thread holds raw
+      scan(std::integral_constant<bool, true>{}, bv, bi);
+    } else {
+      bv = rv;
+      bi = raw;
     }
-    for (int i = 8 * n8 + tid; i < n; i += kT)
-      if (!special(sh, i) && better(cx.one(i), i, bv, bi)) {
-        bv = cx.one(i);
-        bi = i;
-      }
     if (pen_count > 0) {
       const int loc = sh.pen_loc[tid];
       const float v = special_score(loc, pen_count);
@@ -323,7 +344,6 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
         bi = loc;
       }
     }
-    float rv;
     block_argmax(bv, bi, sh, &rv, &local);
     if (local == 0x7fffffff) local = 0;
   } else {
