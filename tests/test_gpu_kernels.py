@@ -225,6 +225,26 @@ def test_gemm_prefill_shapes(torch, yuear_lib, oracle, m, n, k, residual):
     assert_close_bf16(got[rows], ref, scale=scale, exact_frac=0.9)
 
 
+@pytest.mark.parametrize("shape", range(5))
+@pytest.mark.parametrize("m,n,k,residual", [(300, 1000, 512, 0), (517, 776, 192, 1), (1, 200, 64, 1)])
+def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residual):
+    """Each of the five tile shapes, forced, on ragged sizes (M and N not
+    multiples of any tile, N not a multiple of 8, single-row M)."""
+    rng = np.random.default_rng(m + n + shape)
+    a = bf(rng.normal(size=(m, k)))
+    w = bf(rng.normal(size=(n, k)) * 0.05)
+    c0 = bf(rng.normal(size=(m, n))) if residual else np.zeros((m, n), np.uint16)
+    acc = oracle.linear(a, w)
+    ref = bf(f(c0) + f(acc)) if residual else acc
+    da, dw, dc = dev(torch, a), dev(torch, w), dev(torch, c0)
+    assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n, k,
+                                            dc.data_ptr(), n, residual, shape, None) == 0
+    scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+    assert_close_bf16(host(torch, dc), ref, scale=scale, exact_frac=0.9)
+    assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n, k,
+                                            dc.data_ptr(), n, residual, 5, None) == 1
+
+
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])
 def test_gemm_split_k_is_deterministic(torch, yuear_lib, m, n, k):
     """Shapes whose tiles fill less than a round of CUs split K over several

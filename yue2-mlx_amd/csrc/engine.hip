@@ -1820,6 +1820,13 @@ int32_t yuear_op_gemm(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t
   return int32_t(launch_gemm(p, static_cast<hipStream_t>(stream)));
 }
 
+int32_t yuear_op_gemm_tile(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t m,
+                           int32_t n, int32_t k, uint16_t *c, int32_t ldc, int32_t residual,
+                           int32_t shape, void *stream) {
+  GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
+  return int32_t(launch_gemm_tile(p, shape, static_cast<hipStream_t>(stream)));
+}
+
 int32_t yuear_op_attention_prefill(const uint16_t *q, const uint16_t *k_cache,
                                    const uint16_t *v_cache, int32_t tokens, int32_t pos0,
                                    int32_t heads, int32_t kv_heads, int32_t capacity,

@@ -24,7 +24,8 @@
 // Tile shapes (launch_gemm picks the one with the least estimated time for
 // the shape and the CU count): 256 x 256 (8 waves of 128 x 64), 256 x 128 and
 // 128 x 256 (8 waves of 64 x 64), 256 x 192 (8 waves of 64 x 96) and
-// 128 x 128 (4 waves of 64 x 64, two workgroups per CU). At the 3B prefill
+// 128 x 128 (4 waves of 64 x 64, two workgroups per CU); the first three on
+// 16 x 16 x 32 MFMAs (gemm_tile16 below), the others on 32 x 32 x 16. At the 3B prefill
 // shapes (M = 3000) QKV and gate/up take 256 x 256 tiles, the output and down
 // projections (N = 3072, 144 such tiles for 256 CUs) 256 x 192.
 #include <algorithm>
@@ -215,18 +216,151 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
   }
 }
 
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// The same tile on v_mfma_f32_16x16x32_bf16: 16-row fragments (lane l: row
+// l % 16, chunk 4 s + l / 16 of a 32-wide K sub-step s, two sub-steps per
+// step), 16 x 16 accumulators (lane l: token row l % 16, features
+// 4 (l / 16) + [0, 4)). Twice the MFMAs of half the length: measured 6-7 %
+// faster than the 32 x 32 form for 256 x 256 tiles at M = 1024-3000.
+template <int BM, int BN, int WM, int WN>
+__device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int ABLK = BM / 8, BLK = (BM + BN) / 8;
+  constexpr int BPW = BLK / NW;
+  constexpr int STAGE = (BM + BN) * 128;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int q4 = lane >> 4;
+  const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
+  const auto ra = rows_rsrc(p.a + size_t(m0) * p.lda, size_t(p.m - m0) * p.lda * 2);
+  const auto rw = rows_rsrc(p.w + size_t(n0) * p.k, size_t(p.n - n0) * p.k * 2);
+  uint32_t goff[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int q = wave * BPW + i;
+    const bool is_a = q < ABLK;
+    const int row = 8 * (is_a ? q : q - ABLK) + (lane >> 3);
+    const int kc = (lane & 7) ^ (lane >> 3) ^ (q & 1);
+    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8) * 2;
+  }
+  auto dma = [&](int st, int k0) {
+    char *stage = gemm_lds + st * STAGE;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+      const int q = wave * BPW + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q < ABLK ? ra : rw, (lds_ptr_t)(stage + q * 1024),
+                                               16, goff[i] + k0 * 2, 0, 0, 0);
+    }
+  };
+  f32x4v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  const int f = (lane & 7) ^ ((lane >> 3) & 1);
+  const int a_row = (wm * (BM / WM) + (lane & 15)) * 128;
+  const int w_row = BM * 128 + (wn * (BN / WN) + (lane & 15)) * 128;
+  const int steps = p.k / kBK;
+  bf16x8_t af[2][TM], wf[2][TN];
+  auto rd = [&](const char *stage, int buf, int s) {
+    const int co = ((4 * s + q4) ^ f) * 16;
+#pragma unroll
+    for (int x = 0; x < (TM > TN ? TM : TN); ++x) {
+      if (x < TN)
+        wf[buf][x] = *reinterpret_cast<const bf16x8_t *>(stage + w_row + x * 2048 + co);
+      if (x < TM)
+        af[buf][x] = *reinterpret_cast<const bf16x8_t *>(stage + a_row + x * 2048 + co);
+    }
+  };
+  auto mfma = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  dma(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (steps > 1)
+    dma(1, kBK);
+  __syncthreads();
+  rd(gemm_lds, 0, 0);
+  for (int kt = 0; kt < steps; ++kt) {
+    const char *stage = gemm_lds + (kt & 1) * STAGE;
+    rd(stage, 1, 1);
+    mfma(0);
+#pragma unroll
+    for (int q = 0; q < TM + TN; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 2 * (TM + TN), 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    dma(kt & 1, (kt + 2) * kBK);
+    rd(gemm_lds + ((kt + 1) & 1) * STAGE, 0, 0);
+    mfma(1);
+#pragma unroll
+    for (int q = 0; q < TM * TN; ++q) {
+      if (q < BPW)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (q < TM + TN)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * (BM / WM) + i * 16 + (lane & 15);
+    if (m >= p.m)
+      continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * (BN / WN) + j * 16 + 4 * q4;
+      uint16_t *c = p.c + size_t(m) * p.ldc + n;
+      const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (n + 3 < p.n && (p.ldc & 3) == 0) {
+        uint2 o;
+        if (p.residual) {
+          const uint2 old = *reinterpret_cast<const uint2 *>(c);
+          o.x = pack_bf16x2(bf2f(uint16_t(old.x)) + rbf(v[0]), bf2f(uint16_t(old.x >> 16)) + rbf(v[1]));
+          o.y = pack_bf16x2(bf2f(uint16_t(old.y)) + rbf(v[2]), bf2f(uint16_t(old.y >> 16)) + rbf(v[3]));
+        } else {
+          o.x = pack_bf16x2(v[0], v[1]);
+          o.y = pack_bf16x2(v[2], v[3]);
+        }
+        *reinterpret_cast<uint2 *>(c) = o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.n)
+            c[e] = p.residual ? f2bf(bf2f(c[e]) + rbf(v[e])) : f2bf(v[e]);
+      }
+    }
+  }
+}
+
+
 // One kernel per tile shape. The kernels are not templates: this clang emits
 // no host launch stub for these kernel bodies when the kernel itself is a
 // template instantiated from host code.
-#define YUEAR_GEMM_KERNEL(NAME, BM, BN, WM, WN)                                  \
+#define YUEAR_GEMM_KERNEL(NAME, BODY, BM, BN, WM, WN)                            \
   __global__ __launch_bounds__(WM * WN * 64) void NAME(GemmParams p, int tiles_n) { \
-    gemm_tile<BM, BN, WM, WN>(p, tiles_n);                                       \
+    BODY<BM, BN, WM, WN>(p, tiles_n);                                            \
   }
-YUEAR_GEMM_KERNEL(gemm_256x256, 256, 256, 2, 4)
-YUEAR_GEMM_KERNEL(gemm_256x128, 256, 128, 4, 2)
-YUEAR_GEMM_KERNEL(gemm_128x256, 128, 256, 2, 4)
-YUEAR_GEMM_KERNEL(gemm_256x192, 256, 192, 4, 2)
-YUEAR_GEMM_KERNEL(gemm_128x128, 128, 128, 2, 2)
+// MFMA form per shape, as measured: 16 x 16 x 32 for 256 x 256, 256 x 128
+// and 128 x 256; 32 x 32 x 16 for 256 x 192 and 128 x 128 (their 16 x 16
+// forms were equal or slower).
+YUEAR_GEMM_KERNEL(gemm_256x256, gemm_tile16, 256, 256, 2, 4)
+YUEAR_GEMM_KERNEL(gemm_256x128, gemm_tile16, 256, 128, 4, 2)
+YUEAR_GEMM_KERNEL(gemm_128x256, gemm_tile16, 128, 256, 2, 4)
+YUEAR_GEMM_KERNEL(gemm_256x192, gemm_tile, 256, 192, 4, 2)
+YUEAR_GEMM_KERNEL(gemm_128x128, gemm_tile, 128, 128, 2, 2)
 #undef YUEAR_GEMM_KERNEL
 
 // Time model of the tile shapes, in microseconds per 48 K steps measured on

@@ -131,6 +131,9 @@ _SIGS = {
                                       _P(C.c_void_p)]),
     "yuear_op_gemm": (C.c_int32, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                   C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]),
+    "yuear_op_gemm_tile": (C.c_int32, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
+                                       C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                       C.c_void_p]),
     "yuear_op_attention_prefill": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                                C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                                C.c_void_p, C.c_void_p]),
