@@ -274,10 +274,13 @@ int32_t yuear_op_qgemv(const uint32_t *dev_codes, const uint32_t *dev_groups, in
 int32_t yuear_op_dequantize(const uint32_t *dev_codes, const uint32_t *dev_groups,
                             int32_t bits, int32_t n, int32_t k, uint16_t *dev_out,
                             void *stream);
-/* C[m][n] = bf16(A[m] . W[n]), or C = bf16(C + bf16(A[m] . W[n])) when
- * residual (the prefill projections, mx::matmul in ar.cpp:258-298), fp32
- * accumulation on MFMA. k a multiple of 64, lda a multiple of 8, lda >= k,
- * ldc >= n; otherwise hipErrorInvalidValue (1) and nothing is launched. */
+/* C[m][n] = bf16(A[m] . W[n]) (residual 0), C = bf16(C + bf16(A[m] . W[n]))
+ * (residual 1), or, on interleaved gate/up rows W[2i] / W[2i+1], the SwiGLU
+ * pairs C[m][i] = bf16(bf16(silu(g)) * u), g / u = bf16(A[m] . W[2i] / [2i+1])
+ * (residual 2, n even, C [m][n / 2]) -- the prefill projections, mx::matmul
+ * and the mlp of ar.cpp:36-51, 258-298 -- with fp32 accumulation on MFMA.
+ * k a multiple of 64, lda a multiple of 8, lda >= k, ldc >= n (n / 2 for
+ * SwiGLU); otherwise hipErrorInvalidValue (1) and nothing is launched. */
 int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                       int32_t ldc, int32_t residual, void *stream);

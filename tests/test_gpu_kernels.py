@@ -226,6 +226,29 @@ def test_gemm_prefill_shapes(torch, yuear_lib, oracle, m, n, k, residual):
 
 
 @pytest.mark.parametrize("shape", range(5))
+@pytest.mark.parametrize("m,n,k", [(300, 1000, 512), (3000, 16384, 3072), (5, 36, 64)])
+def test_gemm_swiglu_epilogue(torch, yuear_lib, oracle, shape, m, n, k):
+    """The SwiGLU form (residual = 2) on interleaved gate/up rows against the
+    oracle's linear + silu_mul (ar.cpp:36-51), every tile shape; at the
+    3B gate/up shape a sample of rows."""
+    rng = np.random.default_rng(m + shape)
+    a = bf(rng.normal(size=(m, k)))
+    w = bf(rng.normal(size=(n, k)) * 0.03)
+    da, dw = dev(torch, a), dev(torch, w)
+    dc = dev(torch, np.zeros((m, n // 2), np.uint16))
+    assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n, k,
+                                            dc.data_ptr(), n // 2, 2, shape, None) == 0
+    got = host(torch, dc)
+    rows = np.arange(m) if m <= 300 else np.unique(np.r_[0, m - 1, rng.integers(0, m, 40)])
+    acc = oracle.linear(a[rows], w)
+    ref = oracle.silu_mul(acc[:, 0::2], acc[:, 1::2])
+    assert_close_bf16(got[rows], ref, exact_frac=0.9)
+    # odd n is rejected for the SwiGLU form
+    assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n - 1, k,
+                                            dc.data_ptr(), n // 2, 2, shape, None) == 1
+
+
+@pytest.mark.parametrize("shape", range(5))
 @pytest.mark.parametrize("m,n,k,residual", [(300, 1000, 512, 0), (517, 776, 192, 1), (1, 200, 64, 1)])
 def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residual):
     """Each of the five tile shapes, forced, on ragged sizes (M and N not

@@ -277,7 +277,7 @@ struct yuear_session {
   // prefill scratch
   int chunk = 0;
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
-           *pgu = nullptr, *pact = nullptr;
+           *pact = nullptr;
   int32_t *pids = nullptr;
   // host mirrors / pinned
   std::vector<int> host_pos;
@@ -646,7 +646,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.sstate = S.alloc<int32_t>(2 * sets);
   S.history_cap = kContext;
   S.history = S.alloc<int32_t>(size_t(S.history_cap) * sets);
-  // prefill in chunks of up to 4096 tokens (~340 MB of scratch at the 3B
+  // prefill in chunks of up to 4096 tokens (~210 MB of scratch at the 3B
   // shape): larger GEMMs fill the GPU better (M = 3000: 590 TFLOP/s against
   // ~400 at M = 1024) and chunked equals one-pass bit for bit
   S.chunk = std::min(capacity, 4096);
@@ -656,7 +656,6 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.pqkv = S.alloc<uint16_t>(T * c.qkv());
   S.pq = S.alloc<uint16_t>(T * c.Hq * c.D);
   S.pattn = S.alloc<uint16_t>(T * c.Hq * c.D);
-  S.pgu = S.alloc<uint16_t>(T * 2 * c.F);
   S.pact = S.alloc<uint16_t>(T * c.F);
   S.pids = S.alloc<int32_t>(T);
   S.host_pos.assign(branches, 0);
@@ -965,9 +964,8 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
       HIPC(launch_gemm(og, st));
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
-      GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pgu, 2 * c.F, 0};
+      GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pact, c.F, 2};  // SwiGLU epilogue
       HIPC(launch_gemm(gu, st));
-      HIPC(launch_swiglu_rows(S.pgu, T, c.F, S.pact, st));
       GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1};
       HIPC(launch_gemm(dg, st));
     }

@@ -1,7 +1,9 @@
 // Prefill projections on gfx950 MFMA: C[m][n] = bf16(sum_k A[m][k] W[n][k])
 // (A: token rows, W: row-major weights, both K-contiguous), fp32 accumulation
-// with one rounding, or the residual form C = bf16(C + bf16(acc)) with both
-// of the reference's rounding points (native/src/ar.cpp:20-29, 292-298).
+// with one rounding, the residual form C = bf16(C + bf16(acc)) with both of
+// the reference's rounding points (native/src/ar.cpp:20-29, 292-298), or the
+// SwiGLU form C[m][i] = swiglu(acc[m][2 i], acc[m][2 i + 1]) on interleaved
+// gate/up rows (ar.cpp:36-51).
 //
 // Tiling: a workgroup of WM x WN waves computes a BM x BN tile of C; each
 // wave owns (BM / WM) token rows x (BN / WN) features as 32 x 32
@@ -57,6 +59,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void *base, si
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return uint32_t(f2bf(a)) | uint32_t(f2bf(b)) << 16;
+}
+
+// SwiGLU epilogue (ar.cpp:36-51) on interleaved (gate_i, up_i) columns: the
+// lane's features n .. n + 3 (n a multiple of 4) are two pairs, written as
+// outputs n / 2 and n / 2 + 1 of the row with the rounding points of the
+// decode GEMV's epilogue: g, u rounded to bf16, silu(g) rounded, then g * u.
+__device__ __forceinline__ uint16_t swiglu_one(float gate, float up) {
+  const float g = rbf(gate), u = rbf(up);
+  const float act = rbf(g * (1.0f / (1.0f + expf(-g))));
+  return f2bf(act * u);
+}
+__device__ __forceinline__ void swiglu_store(const GemmParams &p, int m, int n, const float *v) {
+  uint16_t *c = p.c + size_t(m) * p.ldc + (n >> 1);
+  if (n + 3 < p.n && (p.ldc & 1) == 0) {
+    *reinterpret_cast<uint32_t *>(c) =
+        uint32_t(swiglu_one(v[0], v[1])) | uint32_t(swiglu_one(v[2], v[3])) << 16;
+  } else {
+    if (n + 1 < p.n)
+      c[0] = swiglu_one(v[0], v[1]);
+    if (n + 3 < p.n)
+      c[1] = swiglu_one(v[2], v[3]);
+  }
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -192,6 +216,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
         uint16_t *c = p.c + size_t(m) * p.ldc + n;
         const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                             acc[i][j][4 * q + 3]};
+        if (p.residual == 2) {
+          swiglu_store(p, m, n, v);
+          continue;
+        }
         if (n + 3 < p.n && (p.ldc & 3) == 0) {
           uint2 o;
           if (p.residual) {
@@ -324,6 +352,10 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
       const int n = n0 + wn * (BN / WN) + j * 16 + 4 * q4;
       uint16_t *c = p.c + size_t(m) * p.ldc + n;
       const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (p.residual == 2) {
+        swiglu_store(p, m, n, v);
+        continue;
+      }
       if (n + 3 < p.n && (p.ldc & 3) == 0) {
         uint2 o;
         if (p.residual) {
@@ -424,8 +456,9 @@ int gemm_tile_choice(int m, int n, int cus) {
 }
 
 hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s) {
-  if (p.m < 1 || p.n < 1 || p.k < kBK || p.k % kBK || p.lda < p.k || p.ldc < p.n ||
-      p.lda % 8 || !p.a || !p.w || !p.c)
+  if (p.m < 1 || p.n < 1 || p.k < kBK || p.k % kBK || p.lda < p.k || p.lda % 8 || !p.a ||
+      !p.w || !p.c || p.residual < 0 || p.residual > 2 || (p.residual == 2 && p.n % 2) ||
+      p.ldc < (p.residual == 2 ? p.n / 2 : p.n))
     return hipErrorInvalidValue;
   switch (shape) {
   case 0: return launch_tile<256, 256, 2, 4>(gemm_256x256, p, s);

@@ -172,7 +172,7 @@ struct GemmParams {
   int m = 0, n = 0, k = 0;
   uint16_t *c = nullptr;        // [m][ldc]
   int ldc = 0;
-  int residual = 0;             // c = bf16(c + bf16(acc))
+  int residual = 0;             // 1: c = bf16(c + bf16(acc)); 2: SwiGLU pairs, c [m][n / 2]
 };
 // MFMA GEMM (gemm.hip); k a multiple of 64, lda a multiple of 8. No scratch.
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
@@ -186,8 +186,6 @@ hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows
 hipError_t launch_rms_norm_rows(const uint16_t *x, int rows, int width,
                                 const uint16_t *w, float eps, uint16_t *y,
                                 hipStream_t s);
-hipError_t launch_swiglu_rows(const uint16_t *gu, int rows, int f, uint16_t *out,
-                              hipStream_t s);
 
 // q/k RMSNorm + RoPE for T tokens at absolute positions pos0 + t; writes q
 // [T][Hq][D] and appends K/V at slots pos0 + t of one branch's cache.

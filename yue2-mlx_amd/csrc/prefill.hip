@@ -1,6 +1,7 @@
-// Prompt prefill kernels on gfx950 (the projections are MFMA GEMMs,
-// gemm.hip): row-wise RMSNorm / embedding / SwiGLU, q/k RMSNorm + RoPE + KV
-// append, and an MFMA causal attention with fp32 opmath.
+// Prompt prefill kernels on gfx950 (the projections are MFMA GEMMs in
+// gemm.hip, SwiGLU in the gate/up GEMM's epilogue): row-wise RMSNorm and
+// embedding, q/k RMSNorm + RoPE + KV append, and an MFMA causal attention
+// with fp32 opmath.
 //
 // Reference: native/src/ar.cpp:246-301 (hidden() over T > 1 tokens) and
 // native/src/sampling.cpp:152-183 (prefill). The reference upcasts Q/K/V to
@@ -69,38 +70,6 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const uint16_t *x, i
   }
 }
 
-// ar.cpp:36-51 on interleaved (gate_i, up_i) columns: 4 pairs (16 bytes in,
-// 8 bytes out) per thread and vector, 4 vectors loaded before the first is
-// used; f a multiple of 4.
-__global__ __launch_bounds__(256) void swiglu_rows_kernel(const uint16_t *gu, int f,
-                                                          uint16_t *out) {
-  const int r = blockIdx.x;
-  const u32x4 *src = reinterpret_cast<const u32x4 *>(gu + size_t(r) * 2 * f);
-  uint2 *dst = reinterpret_cast<uint2 *>(out + size_t(r) * f);
-  constexpr int kIn = 4;  // loads in flight per thread
-  const int nv = f / 4;
-  for (int i0 = threadIdx.x; i0 < nv; i0 += 256 * kIn) {
-    u32x4 v[kIn];
-#pragma unroll
-    for (int k = 0; k < kIn; ++k)
-      v[k] = src[min(i0 + 256 * k, nv - 1)];
-#pragma unroll
-    for (int k = 0; k < kIn; ++k) {
-      const int i = i0 + 256 * k;
-      if (i >= nv)
-        break;
-      const uint32_t pairs[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-      uint32_t o[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float g = bflo(pairs[j]), u = bfhi(pairs[j]);
-        const float act = rbf(g * (1.0f / (1.0f + expf(-g))));
-        o[j] = f2bf(act * u);
-      }
-      dst[i] = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
-    }
-  }
-}
 
 // q/k RMSNorm + RoPE for T tokens, K/V append (ar.cpp:268-282).
 // One workgroup per token; wave w takes heads w, w + 4, ... and issues the
@@ -211,12 +180,6 @@ hipError_t launch_rms_norm_rows(const uint16_t *x, int rows, int width, const ui
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_rows(const uint16_t *gu, int rows, int f, uint16_t *out, hipStream_t s) {
-  if (rows < 1 || f < 4 || f % 4)
-    return hipErrorInvalidValue;
-  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(rows), dim3(256), 0, s, gu, f, out);
-  return hipGetLastError();
-}
 
 hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
   if (p.head_dim != 128 || p.tokens < 1 || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity ||
