@@ -307,7 +307,12 @@ int32_t yuear_op_attention_prefill(const uint16_t *dev_q,
  * times scale * log2(e), exp2 softmax, fp32 P.V, bf16(o / l); causal hides
  * the keys after each query (q_len == kv_len). query_chunk_size is validated
  * as in the reference and does not change the result (every query sees the
- * same keys in one pass). workspace: yuear_nar_attention_workspace_bytes()
+ * same keys in one pass). The reference runs its Metal kernel only for
+ * non-causal calls with q_len > 8 and query_chunk_size >= 64; its other
+ * calls go to MLX's sdpa (bf16 operands for chunks of <= 8 queries, fp32
+ * otherwise, nar_attention.cpp:245-268). This entry point computes those
+ * with the same precise kernel too: their parity with the reference is
+ * unpinned. workspace: yuear_nar_attention_workspace_bytes()
  * of device memory. A non-causal launch too small to fill the GPU splits
  * its keys over workgroups; the split partials come from a library pool
  * per (device, stream). So the first such call on a stream, or one that

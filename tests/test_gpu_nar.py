@@ -46,6 +46,11 @@ def host(torch, t):
     (1, 24, 8, 2050, 2050, True),
     (32, 24, 8, 64, 1, False),     # 768 workgroups of 64 queries over one key
     (16, 24, 8, 130, 130, True),   # 1152 workgroups, causal, 2-query last tiles
+    # keys split over workgroups (fewer than 768 workgroups of 64 queries)
+    (1, 16, 8, 64, 2570, False),   # 81 key blocks: 9 splits of 9, none empty
+    (1, 24, 8, 512, 3512, False),  # the benchmarked acoustic chunk over conditioning keys
+    (1, 16, 8, 4, 3100, False),    # 4 queries in one 64-query tile, 12 splits
+    (2, 16, 8, 100, 1500, False),  # batch 2, 5 splits, ragged last query tile
 ])
 def test_nar_attention_matches_oracle(torch, yuear_lib, oracle, B, Hq, Hkv, Lq, Lk, causal):
     print(f"[nar] B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} causal={causal}", flush=True)
@@ -135,3 +140,34 @@ def test_nar_condition_is_the_prefill_cache(torch, yuear_lib, oracle):
     with pytest.raises(ValueError, match="quantized AR cannot condition NAR"):
         q.nar_condition([1, 2, 3])
     q.close()
+
+
+def test_nar_attention_graph_survives_a_larger_call(torch, yuear_lib):
+    """The split partials come from a pool per (device, stream). A graph
+    captured on a stream keeps the pool buffer it was captured with: a later
+    call on that stream that needs a larger buffer allocates a new one and
+    keeps the old one alive, so replays of the graph stay correct."""
+    rng = np.random.default_rng(21)
+
+    def inputs(lk):
+        return (dev(torch, bf(rng.normal(size=(1, 16, 64, 128)))),
+                dev(torch, bf(rng.normal(size=(1, 8, lk, 128)))),
+                dev(torch, bf(rng.normal(size=(1, 8, lk, 128)))))
+
+    small, large = inputs(600), inputs(2570)  # 2 and 9 key splits
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        ws = torch.empty(yuear_lib.lib.yuear_nar_attention_workspace_bytes(1, 8, 2570) // 2,
+                         dtype=torch.bfloat16, device="cuda")
+        want = yuear_lib.nar_attention(*small, workspace=ws, stream=s.cuda_stream)
+        want = host(torch, want)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = yuear_lib.nar_attention(*small, workspace=ws, stream=s.cuda_stream)
+        big = host(torch, yuear_lib.nar_attention(*large, workspace=ws, stream=s.cuda_stream))
+        for replay in range(3):
+            out.zero_()
+            g.replay()
+            np.testing.assert_array_equal(host(torch, out), want, err_msg=f"replay {replay}")
+    again = host(torch, yuear_lib.nar_attention(*large, workspace=ws, stream=s.cuda_stream))
+    np.testing.assert_array_equal(again, big)
