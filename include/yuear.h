@@ -342,6 +342,68 @@ yuear_status yuear_nar_attention(const uint16_t *dev_q, const uint16_t *dev_k,
 void yuear_rope_table(int32_t positions, int32_t head_dim, double theta,
                       uint16_t *cos_out, uint16_t *sin_out);
 
+/* ---- text side of a request (host only): the prompt prefixes the decode
+ * loop is given (protocol.hpp:5-24, protocol.mm:123-357, 428-591) ---- */
+typedef struct yuear_tokenizer yuear_tokenizer;
+/* lyra::Tokenizer(vocabulary) (protocol.mm:438-485): a checkpoint-native
+ * qwen.tiktoken, one "base64-piece rank" line per ordinary token, exactly
+ * 151643 of them (ranks [0, 151643)); the special and <extra_i> pieces
+ * follow. Errors: FileNotFoundError / PermissionError / OSError, ValueError
+ * with the reference's messages. */
+yuear_status yuear_tokenizer_load(const char *vocabulary, yuear_tokenizer **out,
+                                  char **error_json);
+void yuear_tokenizer_destroy(yuear_tokenizer *tokenizer);
+/* Tokenizer::encode (protocol.mm:558-579): `len` bytes of UTF-8 (NUL bytes
+ * allowed) -> NFC -> the reference's pre-tokenizer pattern -> byte pair
+ * merges. *ids is allocated by the library (free with yuear_ids_free), *n
+ * its length. Invalid UTF-8: UnicodeDecodeError "Invalid UTF-8 text". */
+yuear_status yuear_tokenizer_encode(const yuear_tokenizer *tokenizer, const char *text,
+                                    int64_t len, int32_t **ids, int64_t *n, char **error_json);
+/* Tokenizer::decode (protocol.mm:580-591): ids outside the text vocabulary
+ * are skipped, invalid UTF-8 becomes U+FFFD per maximal subpart. *text is
+ * NUL-terminated (free with yuear_string_free), *len its byte length
+ * (len may be NULL). */
+yuear_status yuear_tokenizer_decode(const yuear_tokenizer *tokenizer, const int32_t *ids,
+                                    int64_t n, char **text, int64_t *len, char **error_json);
+void yuear_ids_free(int32_t *ids);
+/* Test hooks (no counterpart in the reference) for the two stages inside
+ * encode: the NFC form of UTF-8 text (as yuear_tokenizer_decode returns
+ * text), and the pre-tokenizer's pieces of that NFC text as the byte offset
+ * where each ends (as yuear_tokenizer_encode returns ids). */
+yuear_status yuear_text_nfc(const char *text, int64_t len, char **out, int64_t *out_len,
+                            char **error_json);
+yuear_status yuear_text_pieces(const char *text, int64_t len, int32_t **ends, int64_t *n,
+                               char **error_json);
+/* The SongRequest fields the prompt layout reads (protocol.hpp SongRequest):
+ * NUL-terminated UTF-8; abc NULL when absent; has_cfg_scale 0 when absent. */
+typedef struct yuear_song_request {
+  const char *style, *lyrics, *cot, *abc, *id;
+  uint64_t seed;
+  double cfg_scale;
+  int32_t has_cfg_scale;
+} yuear_song_request;
+/* SongRequest::validate (protocol.mm:212-237), same ValueError messages. */
+yuear_status yuear_song_request_validate(const yuear_song_request *request, char **error_json);
+/* SongRequest::guidance (protocol.mm:238-240): cfg_scale, else 1.01 for
+ * cot "off" and 1 otherwise. */
+double yuear_song_request_guidance(const yuear_song_request *request);
+/* token_prefixes(request, tokenizer, abc_ids) (protocol.mm:321-340):
+ * [EOD] + encode(text) + [ABC_START], then for cot "off" [ABC_END,
+ * MUSIC_START]; otherwise, when abc_ids are given (has_abc_ids) or the
+ * request carries abc text, the ABC ids + [ABC_END, MUSIC_START]. Output as
+ * yuear_tokenizer_encode. */
+yuear_status yuear_token_prefixes(const yuear_tokenizer *tokenizer,
+                                  const yuear_song_request *request, const int32_t *abc_ids,
+                                  int64_t n_abc, int32_t has_abc_ids, int32_t **ids, int64_t *n,
+                                  char **error_json);
+/* negative_prefix(request, tokenizer, abc_ids) (protocol.mm:341-357): the
+ * unconditional CFG branch, [EOD] + encode(instruction) + the same tail
+ * (cot "off": [MUSIC_START]; otherwise abc_ids are required). */
+yuear_status yuear_negative_prefix(const yuear_tokenizer *tokenizer,
+                                   const yuear_song_request *request, const int32_t *abc_ids,
+                                   int64_t n_abc, int32_t has_abc_ids, int32_t **ids, int64_t *n,
+                                   char **error_json);
+
 #ifdef __cplusplus
 }
 #endif

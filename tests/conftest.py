@@ -24,6 +24,17 @@ MODEL_3B = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
                qk_norm=True)
 
 
+@pytest.fixture(scope="session")
+def text_vocab(tmp_path_factory):
+    """(path, ranks) of the test qwen.tiktoken (text_util.vocabulary_pieces)."""
+    import text_ref
+    import text_util
+    pieces = text_util.vocabulary_pieces()
+    path = tmp_path_factory.mktemp("vocab") / "qwen.tiktoken"
+    text_ref.write_vocabulary(path, pieces)
+    return str(path), {p: r for r, p in enumerate(pieces)}
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD Instinct GPU (gfx950) through HIP")
 

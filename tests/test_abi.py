@@ -98,12 +98,51 @@ def test_sampling_struct_defaults_follow_reference(yuear_lib):
 def test_cxx_facade_compiles_and_links(tmp_path):
     """include/yuear.hpp (the C++20 facade with the reference's
     generate_tokens signature) and its driver build against libyuear.so."""
-    out = tmp_path / "facade"
-    subprocess.run(["g++", "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror",
-                    "-I" + os.path.join(ROOT, "include"),
-                    os.path.join(ROOT, "tests", "cxx", "facade_test.cpp"), "-o", str(out),
-                    "-L" + os.path.dirname(LIB), "-lyuear"], check=True)
-    assert out.exists()
+    for name in ("facade_test", "pipeline_test"):
+        out = tmp_path / name
+        subprocess.run(["g++", "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror",
+                        "-I" + os.path.join(ROOT, "include"),
+                        os.path.join(ROOT, "tests", "cxx", name + ".cpp"), "-o", str(out),
+                        "-L" + os.path.dirname(LIB), "-lyuear"], check=True)
+        assert out.exists()
+
+
+def test_cxx_facade_errors_keep_their_type(tmp_path, text_vocab):
+    """Errors raised by library calls reach a C++ caller as yuear::Error with
+    the library's type and message (host-only calls: no GPU needed)."""
+    src = r'''
+#include "yuear.hpp"
+#include <cstdio>
+template <class F> void expect(F f) {
+  try { f(); std::printf("none\n"); }
+  catch (const yuear::Error &e) { std::printf("%s: %s\n", e.type.c_str(), e.what()); }
+}
+int main(int, char **argv) {
+  expect([] { yuear::Tokenizer t("/nonexistent/qwen.tiktoken"); });
+  yuear::SongRequest r;
+  r.style = "a";
+  r.lyrics = "b";
+  r.id = "../x";
+  expect([&] { r.validate(); });
+  const yuear::Tokenizer t(argv[1]);
+  expect([&] { t.encode("ok\xff"); });
+  r.id = "song";
+  expect([&] { yuear::negative_prefix(r, t); });
+  std::printf("%s|%d\n", t.decode(t.encode("Hello")).c_str(), int(yuear::token_prefixes(r, t).back()));
+}
+'''
+    cpp, exe = tmp_path / "t.cpp", tmp_path / "t"
+    cpp.write_text(src)
+    subprocess.run(["g++", "-std=c++20", "-I" + os.path.join(ROOT, "include"), str(cpp), "-o",
+                    str(exe), "-L" + os.path.dirname(LIB), "-lyuear",
+                    "-Wl,-rpath," + os.path.dirname(LIB)], check=True)
+    out = subprocess.run([str(exe), text_vocab[0]], capture_output=True, text=True,
+                         check=True).stdout.splitlines()
+    assert out[0].startswith("FileNotFoundError: /nonexistent/qwen.tiktoken")
+    assert out[1] == "ValueError: id must be a filename-safe identifier"
+    assert out[2] == "UnicodeDecodeError: Invalid UTF-8 text"
+    assert out[3] == "ValueError: Symbolic CFG must retain the exact positive-branch ABC IDs"
+    assert out[4] == "Hello|151847"
 
 
 def test_cxx_facade_error_json_parser():

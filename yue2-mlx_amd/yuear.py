@@ -56,6 +56,12 @@ class WeightSource(C.Structure):
                 ("bits", C.c_int32)]
 
 
+class SongRequestC(C.Structure):
+    _fields_ = [("style", C.c_char_p), ("lyrics", C.c_char_p), ("cot", C.c_char_p),
+                ("abc", C.c_char_p), ("id", C.c_char_p), ("seed", C.c_uint64),
+                ("cfg_scale", C.c_double), ("has_cfg_scale", C.c_int32)]
+
+
 TOKEN_CB = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int32)
 
 lib = C.CDLL(LIB_PATH)
@@ -137,6 +143,23 @@ _SIGS = {
     "yuear_op_attention_prefill": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
                                                C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                                C.c_void_p, C.c_void_p]),
+    "yuear_tokenizer_load": (C.c_int, [C.c_char_p, _P(C.c_void_p), _P(C.c_void_p)]),
+    "yuear_tokenizer_destroy": (None, [C.c_void_p]),
+    "yuear_tokenizer_encode": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int64, _P(i32p),
+                                         _P(C.c_int64), _P(C.c_void_p)]),
+    "yuear_tokenizer_decode": (C.c_int, [C.c_void_p, i32p, C.c_int64, _P(C.c_void_p),
+                                         _P(C.c_int64), _P(C.c_void_p)]),
+    "yuear_ids_free": (None, [i32p]),
+    "yuear_text_nfc": (C.c_int, [C.c_char_p, C.c_int64, _P(C.c_void_p), _P(C.c_int64),
+                                 _P(C.c_void_p)]),
+    "yuear_text_pieces": (C.c_int, [C.c_char_p, C.c_int64, _P(i32p), _P(C.c_int64),
+                                    _P(C.c_void_p)]),
+    "yuear_song_request_validate": (C.c_int, [_P(SongRequestC), _P(C.c_void_p)]),
+    "yuear_song_request_guidance": (C.c_double, [_P(SongRequestC)]),
+    "yuear_token_prefixes": (C.c_int, [C.c_void_p, _P(SongRequestC), i32p, C.c_int64, C.c_int32,
+                                       _P(i32p), _P(C.c_int64), _P(C.c_void_p)]),
+    "yuear_negative_prefix": (C.c_int, [C.c_void_p, _P(SongRequestC), i32p, C.c_int64,
+                                        C.c_int32, _P(i32p), _P(C.c_int64), _P(C.c_void_p)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -156,12 +179,18 @@ def _take_error(err):
         return {"type": "RuntimeError", "message": text}
 
 
+class TextDecodeError(ValueError):
+    """The library's UnicodeDecodeError (invalid UTF-8 input text)."""
+
+
 def _check(status, err):
     if status == 0:
         return
     info = _take_error(err)
     kind = {"ValueError": ValueError, "InterruptedError": InterruptedError,
-            "FileNotFoundError": FileNotFoundError}.get(info.get("type"), RuntimeError)
+            "FileNotFoundError": FileNotFoundError, "PermissionError": PermissionError,
+            "OSError": OSError, "UnicodeDecodeError": TextDecodeError,
+            "MemoryError": MemoryError}.get(info.get("type"), RuntimeError)
     if status == 130:
         kind = InterruptedError
     raise kind(info.get("message", ""))
@@ -585,3 +614,120 @@ class Session:
         err = C.c_void_p()
         _check(lib.yuear_session_time_steps(self._h(), steps, C.byref(ms), C.byref(err)), err)
         return ms.value
+
+
+# ---- text side of a request (host only, no GPU): protocol.hpp / protocol.mm ----
+
+def _ids_out(ptr, n):
+    ids = [ptr[i] for i in range(n.value)]
+    lib.yuear_ids_free(ptr)
+    return ids
+
+
+def _ids_in(ids):
+    arr = np.ascontiguousarray(np.asarray(list(ids) if ids is not None else [], dtype=np.int32))
+    return arr, arr.ctypes.data_as(i32p)
+
+
+class Tokenizer:
+    """lyra::Tokenizer (protocol.hpp:5-16): ``encode(text) -> ids`` and
+    ``decode(ids) -> text`` over a checkpoint-native qwen.tiktoken."""
+
+    def __init__(self, vocabulary):
+        self._t = C.c_void_p()
+        err = C.c_void_p()
+        _check(lib.yuear_tokenizer_load(os.fsencode(vocabulary), C.byref(self._t), C.byref(err)),
+               err)
+
+    def close(self):
+        if self._t:
+            lib.yuear_tokenizer_destroy(self._t)
+            self._t = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text):
+        data = text.encode("utf-8", errors="surrogatepass") if isinstance(text, str) else bytes(text)
+        ptr, n, err = i32p(), C.c_int64(), C.c_void_p()
+        _check(lib.yuear_tokenizer_encode(self._t, data, len(data), C.byref(ptr), C.byref(n),
+                                          C.byref(err)), err)
+        return _ids_out(ptr, n)
+
+    def decode(self, ids):
+        arr, p = _ids_in(ids)
+        out, n, err = C.c_void_p(), C.c_int64(), C.c_void_p()
+        _check(lib.yuear_tokenizer_decode(self._t, p, arr.size, C.byref(out), C.byref(n),
+                                          C.byref(err)), err)
+        text = C.string_at(out, n.value).decode("utf-8")
+        lib.yuear_string_free(out)
+        return text
+
+
+def text_nfc(text):
+    """Test hook: the library's NFC of `text` (str or UTF-8 bytes)."""
+    data = text.encode("utf-8", errors="surrogatepass") if isinstance(text, str) else bytes(text)
+    out, n, err = C.c_void_p(), C.c_int64(), C.c_void_p()
+    _check(lib.yuear_text_nfc(data, len(data), C.byref(out), C.byref(n), C.byref(err)), err)
+    value = C.string_at(out, n.value).decode("utf-8")
+    lib.yuear_string_free(out)
+    return value
+
+
+def text_pieces(text):
+    """Test hook: the pre-tokenizer's pieces (str) of the NFC form of `text`."""
+    data = text.encode("utf-8", errors="surrogatepass") if isinstance(text, str) else bytes(text)
+    ptr, n, err = i32p(), C.c_int64(), C.c_void_p()
+    _check(lib.yuear_text_pieces(data, len(data), C.byref(ptr), C.byref(n), C.byref(err)), err)
+    ends = _ids_out(ptr, n)
+    nfc = text_nfc(data).encode("utf-8")
+    return [nfc[a:b].decode("utf-8") for a, b in zip([0] + ends[:-1], ends)]
+
+
+class SongRequest:
+    """The SongRequest fields the prompt layout reads (types.hpp:50-62;
+    defaults cot "full", seed 831001, id "song")."""
+
+    def __init__(self, style, lyrics, cot="full", seed=831001, abc=None, cfg_scale=None,
+                 id="song"):
+        self.style, self.lyrics, self.cot, self.seed = style, lyrics, cot, seed
+        self.abc, self.cfg_scale, self.id = abc, cfg_scale, id
+
+    def _c(self):
+        enc = (lambda v: None if v is None else v.encode("utf-8"))
+        return SongRequestC(enc(self.style), enc(self.lyrics), enc(self.cot), enc(self.abc),
+                            enc(self.id), int(self.seed),
+                            0.0 if self.cfg_scale is None else float(self.cfg_scale),
+                            int(self.cfg_scale is not None))
+
+    def validate(self):
+        err = C.c_void_p()
+        r = self._c()
+        _check(lib.yuear_song_request_validate(C.byref(r), C.byref(err)), err)
+
+    @property
+    def guidance(self):
+        r = self._c()
+        return lib.yuear_song_request_guidance(C.byref(r))
+
+
+def _prefix(fn, tokenizer, request, abc_ids):
+    arr, p = _ids_in(abc_ids)
+    r = request._c()
+    ptr, n, err = i32p(), C.c_int64(), C.c_void_p()
+    _check(fn(tokenizer._t, C.byref(r), p, arr.size, int(abc_ids is not None), C.byref(ptr),
+              C.byref(n), C.byref(err)), err)
+    return _ids_out(ptr, n)
+
+
+def token_prefixes(request, tokenizer, abc_ids=None):
+    """token_prefixes (protocol.mm:321-340)."""
+    return _prefix(lib.yuear_token_prefixes, tokenizer, request, abc_ids)
+
+
+def negative_prefix(request, tokenizer, abc_ids=None):
+    """negative_prefix (protocol.mm:341-357)."""
+    return _prefix(lib.yuear_negative_prefix, tokenizer, request, abc_ids)
