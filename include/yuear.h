@@ -385,7 +385,7 @@ typedef struct yuear_song_request {
 /* SongRequest::validate (protocol.mm:212-237), same ValueError messages. */
 yuear_status yuear_song_request_validate(const yuear_song_request *request, char **error_json);
 /* SongRequest::guidance (protocol.mm:238-240): cfg_scale, else 1.01 for
- * cot "off" and 1 otherwise. */
+ * cot "off" and 1 otherwise (1 for a NULL request). */
 double yuear_song_request_guidance(const yuear_song_request *request);
 /* token_prefixes(request, tokenizer, abc_ids) (protocol.mm:321-340):
  * [EOD] + encode(text) + [ABC_START], then for cot "off" [ABC_END,

@@ -678,6 +678,8 @@ yuear_status yuear_song_request_validate(const yuear_song_request *r, char **err
 }
 
 double yuear_song_request_guidance(const yuear_song_request *r) {
+  if (!r)
+    return 1.;
   if (r->has_cfg_scale)
     return r->cfg_scale;
   return r->cot && std::string(r->cot) == "off" ? 1.01 : 1.;
