@@ -414,7 +414,8 @@ def main():
         cpu_ref.lib().oracle_set_threads(threads)
         model = cpu_ref.Model(c, weights, bits=bits)
         L0 = args.kv - 1
-        cache = model.cache(L0 + 64)
+        cap = 256  # steps at most; --cpu-seconds ends the sample first on a 16-thread host
+        cache = model.cache(L0 + cap + 1)
         for layer in range(c["num_hidden_layers"]):
             k, v = session.read_kv(layer, 0, L0)
             cache.keys(layer)[:, :L0] = k
@@ -422,7 +423,7 @@ def main():
         cache.offset = L0
         token, n = int(tokens[-1]), 0
         t = time.perf_counter()
-        while n < 60 and (n < 2 or time.perf_counter() - t < args.cpu_seconds):
+        while n < cap and (n < 2 or time.perf_counter() - t < args.cpu_seconds):
             logits = model.step(token, cache)
             token = int(cpu_ref.bf16_to_f32(logits).argmax())
             n += 1
