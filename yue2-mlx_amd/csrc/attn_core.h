@@ -1,6 +1,6 @@
-// Split-K decode attention core for head_dim 128 on gfx950 MFMA, shared by
-// the per-op kernel (attention.hip) and the persistent step (decode.hip):
-// both call these functions, so the two decode paths compute the same bits.
+// Split-K decode attention core for head_dim 128 on gfx950 MFMA: the
+// per-split math of the decode attention kernel (attention.hip, whose
+// workgroup body is attn_block.h).
 //
 // Reference: native/src/ar.cpp:268-291 (q/k RMSNorm, RoPE, SDPA with fp32
 // softmax and accumulation) and ar.cpp:88-91.

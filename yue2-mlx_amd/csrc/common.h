@@ -207,8 +207,8 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 // Split-K merge weight of split t, held by lane t (active: t < n_active):
 // f_t / sum_s f_s l_s with f_t = exp2(m_t - max_s m_s) (log2(e) is folded
-// into the scores) and l_t the split's softmax denominator. Shared by both
-// decode paths so that their merges agree bit for bit.
+// into the scores) and l_t the split's softmax denominator (the decode
+// attention's last-arriving workgroup, attn_block.h).
 __device__ __forceinline__ float merge_weight(float m, float l, bool active) {
   const float mm = active ? m : -__builtin_inff();
   const float M = wave_max(mm);
