@@ -95,7 +95,16 @@ def check_fidelity(gpu, oracle32, oracle64):
     agrees unless the top two are closer than that radius."""
     radius = fidelity_metrics(oracle32, oracle64)
     got = fidelity_metrics(gpu, oracle64)
-    print("oracle radius", radius, "gpu", got)
+    # the per-logit bound of the single-layer tests (2e-2 abs + 1e-2 rel),
+    # reported here: the share of logits inside it, GPU and fp32 oracle
+    ref = _f64(oracle64)
+    bound = 2e-2 + 1e-2 * np.abs(ref)
+    within = {"gpu": float(np.mean(np.abs(_f64(gpu) - ref) <= bound)),
+              "oracle32": float(np.mean(np.abs(_f64(oracle32) - ref) <= bound))}
+    print("oracle radius", radius, "gpu", got, "within 2e-2 + 1e-2 rel", within, flush=True)
+    # at 28 layers both shares sit near 0.5-0.8 (measured); the GPU's may not
+    # fall far below the fp32 oracle's own
+    assert within["gpu"] >= 0.7 * within["oracle32"], within
     assert got["max_abs"] <= 2 * radius["max_abs"]
     assert got["rms"] <= 2 * radius["rms"]
     assert 1 - got["cos"] <= 2 * (1 - radius["cos"])
