@@ -71,10 +71,13 @@ hipError_t launch_gemv(const GemvParams &p, hipStream_t s) {
   // Rows per wave. Batch 1: one row (QKV 5120 rows = 1280 workgroups, o_proj
   // 768, lm_head 20992: whole multiples of the 256 CUs, measured 4-7% faster
   // per launch than two rows on MI355X); the SwiGLU epilogue needs its
-  // (gate, up) pair in one wave. Batch 2: two rows keep ~12 KiB of weight
-  // loads in flight per wave at K = 3072; K = 8192 uses one row.
+  // (gate, up) pair in one wave. Batch 2: one row as well (QKV 9.1 against
+  // 9.4 us, o_proj 6.1 against 6.8), except for the lm_head-sized grids,
+  // where two rows keep ~12 KiB of weight loads in flight per wave
+  // (73 against 77 us); K = 8192 uses one row.
   const bool wide = p.k > 4096;
-  const bool two = p.epilogue == kEpiSwiGLU || (p.batch > 1 && !wide);
+  const bool two = p.epilogue == kEpiSwiGLU ||
+                   (!wide && (p.batch > 2 || (p.batch == 2 && p.n >= 32768)));
   if (p.batch == 1) return two ? launch_b<1, 2>(p, s) : launch_b<1, 1>(p, s);
   if (p.batch == 2) return two ? launch_b<2, 2>(p, s) : launch_b<2, 1>(p, s);
   if (p.batch <= 4) return two ? launch_b<4, 2>(p, s) : launch_b<4, 1>(p, s);

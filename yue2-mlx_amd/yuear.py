@@ -419,9 +419,11 @@ class Engine:
         self.handle = handle
         return self
 
-    def close(self):
+    def close(self, _destroy=lib.yuear_engine_destroy):
+        # _destroy is bound at definition: at interpreter exit the module's
+        # globals may already be gone when __del__ runs
         if getattr(self, "handle", None):
-            lib.yuear_engine_destroy(self.handle)
+            _destroy(self.handle)
             self.handle = None
 
     __del__ = close
@@ -508,9 +510,9 @@ class Session:
         self.handle = handle
         self.vocab = lib.yuear_session_phase_size(handle)
 
-    def close(self):
+    def close(self, _end=lib.yuear_session_end):
         if getattr(self, "handle", None):
-            lib.yuear_session_end(self.handle)
+            _end(self.handle)
             self.handle = None
 
     __del__ = close
@@ -639,9 +641,9 @@ class Tokenizer:
         _check(lib.yuear_tokenizer_load(os.fsencode(vocabulary), C.byref(self._t), C.byref(err)),
                err)
 
-    def close(self):
-        if self._t:
-            lib.yuear_tokenizer_destroy(self._t)
+    def close(self, _destroy=lib.yuear_tokenizer_destroy):
+        if getattr(self, "_t", None):
+            _destroy(self._t)
             self._t = C.c_void_p()
 
     def __del__(self):
