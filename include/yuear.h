@@ -403,6 +403,13 @@ yuear_status yuear_negative_prefix(const yuear_tokenizer *tokenizer,
                                    const yuear_song_request *request, const int32_t *abc_ids,
                                    int64_t n_abc, int32_t has_abc_ids, int32_t **ids, int64_t *n,
                                    char **error_json);
+/* chunk_ranges(frames, prefix_tokens, context) (protocol.mm:358-369): the
+ * acoustic stage's frame chunks [a, b) of min((context - prefix - 3) / 2,
+ * 24576) frames each; *bounds receives n pairs (a, b) as 2 n ints (free
+ * with yuear_ids_free). ValueError "Empty codec or prefix leaves no
+ * acoustic context" when frames < 1 or context - prefix - 3 < 2. */
+yuear_status yuear_chunk_ranges(int32_t frames, int32_t prefix_tokens, int32_t context,
+                                int32_t **bounds, int64_t *n, char **error_json);
 
 #ifdef __cplusplus
 }

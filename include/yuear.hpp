@@ -9,8 +9,8 @@
 //                                                   (ar.hpp:43-48)
 //   lyra::Error{type, message}                    -> yuear::Error (types.hpp:20-24)
 //   lyra::Sampling defaults                       -> yuear::Sampling (types.hpp:29-38)
-//   lyra::Tokenizer, token_prefixes, negative_prefix, SongRequest
-//                                                 -> yuear::Tokenizer, ... (protocol.hpp:5-24,
+//   lyra::Tokenizer, token_prefixes, negative_prefix, chunk_ranges,
+//   SongRequest                                   -> yuear::Tokenizer, ... (protocol.hpp:5-26,
 //                                                   types.hpp:50-62)
 //   Pipeline::generate_phase / plan / generate_semantic
 //                                                 -> yuear::Pipeline (pipeline.cpp:186-263)
@@ -302,6 +302,20 @@ inline std::vector<int> token_prefixes(const SongRequest &r, const Tokenizer &t,
 inline std::vector<int> negative_prefix(const SongRequest &r, const Tokenizer &t,
                                         const std::optional<std::vector<int>> &abc_ids = {}) {
   return detail::prefix(yuear_negative_prefix, r, t, abc_ids);
+}
+
+// chunk_ranges (protocol.hpp:25-26, protocol.mm:358-369)
+inline std::vector<std::pair<int, int>> chunk_ranges(int frames, int prefix_tokens,
+                                                     int context = 24576) {
+  int32_t *bounds = nullptr;
+  int64_t n = 0;
+  char *error = nullptr;
+  detail::check(yuear_chunk_ranges(frames, prefix_tokens, context, &bounds, &n, &error), error);
+  std::vector<std::pair<int, int>> out;
+  for (int64_t i = 0; i < n; ++i)
+    out.emplace_back(bounds[2 * i], bounds[2 * i + 1]);
+  yuear_ids_free(bounds);
+  return out;
 }
 
 // GenerationConfig's per-phase sampling defaults (vendor protocol.py:44-47;

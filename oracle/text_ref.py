@@ -12,7 +12,8 @@ imported by tests, never by the product library.
   U+0085 (``VENDOR_PATTERN``).
 - decode (protocol.mm:580-591): pieces joined, ``bytes.decode(errors="replace")``.
 - the prompt layout: instruction, SongRequest.text, token_prefixes,
-  negative_prefix, guidance (protocol.mm:200-357; vendor protocol.py:104-138).
+  negative_prefix, guidance, chunk_ranges (protocol.mm:200-369; vendor
+  protocol.py:104-145).
 """
 from __future__ import annotations
 
@@ -114,3 +115,14 @@ def negative_prefix(cot, ranks, abc_ids=None):
     if cot == "off":
         return base + [MUSIC_START]
     return base + [ABC_START] + list(abc_ids) + [ABC_END, MUSIC_START]
+
+
+CONTEXT = 24576
+
+
+def chunk_ranges(frames, prefix_tokens, context=CONTEXT):
+    """The acoustic stage's frame chunks (vendor protocol.py:141-145)."""
+    size = min((context - prefix_tokens - 3) // 2, CONTEXT)
+    if frames < 1 or size < 1:
+        raise ValueError("Empty codec or prefix leaves no acoustic context")
+    return [(a, min(a + size, frames)) for a in range(0, frames, size)]

@@ -129,6 +129,9 @@ int main(int, char **argv) {
   r.id = "song";
   expect([&] { yuear::negative_prefix(r, t); });
   std::printf("%s|%d\n", t.decode(t.encode("Hello")).c_str(), int(yuear::token_prefixes(r, t).back()));
+  const auto chunks = yuear::chunk_ranges(7, 10, 20);
+  std::printf("%zu|%d|%d\n", chunks.size(), chunks.back().first, chunks.back().second);
+  expect([] { yuear::chunk_ranges(0, 10); });
 }
 '''
     cpp, exe = tmp_path / "t.cpp", tmp_path / "t"
@@ -143,6 +146,8 @@ int main(int, char **argv) {
     assert out[2] == "UnicodeDecodeError: Invalid UTF-8 text"
     assert out[3] == "ValueError: Symbolic CFG must retain the exact positive-branch ABC IDs"
     assert out[4] == "Hello|151847"
+    assert out[5] == "3|6|7"
+    assert out[6] == "ValueError: Empty codec or prefix leaves no acoustic context"
 
 
 def test_cxx_facade_error_json_parser():

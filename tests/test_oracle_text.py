@@ -127,3 +127,14 @@ def test_decode_is_python_replacement_decoding(text_vocab):
     split = [ranks[euro[:1]], ranks[euro[1:2]]]  # a cut three-byte character
     assert text_ref.decode(split, ranks) == "�"
     assert text_ref.decode([ranks[b"a"], EOD, ABC_START, 10 ** 7, -1], ranks) == "a<|endoftext|><abc>"
+
+
+def test_chunk_ranges_hand_worked():
+    # (context - prefix - 3) // 2 frames per chunk, capped at the context
+    assert text_ref.chunk_ranges(10, 24570) == [(i, i + 1) for i in range(10)]  # 3 // 2 = 1
+    assert text_ref.chunk_ranges(5000, 100) == [(0, 5000)]                       # 12236 per chunk
+    assert text_ref.chunk_ranges(30000, 0) == [(0, 12286), (12286, 24572), (24572, 30000)]
+    assert text_ref.chunk_ranges(7, 10, context=20) == [(0, 3), (3, 6), (6, 7)]  # 7 // 2 = 3
+    for frames, prefix in ((0, 10), (5, 24572), (5, 30000)):
+        with pytest.raises(ValueError, match="Empty codec or prefix leaves no acoustic context"):
+            text_ref.chunk_ranges(frames, prefix)

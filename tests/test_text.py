@@ -226,3 +226,26 @@ def test_request_validation_and_guidance(yuear, tok):
     yuear.SongRequest("a", "b", id="A9_.-x" + "b" * 174, abc=" x ", cfg_scale=20).validate()
     with pytest.raises(ValueError, match="cot must be off, melody or full"):
         yuear.token_prefixes(yuear.SongRequest("a", "b", cot="x"), tok)
+
+
+def test_chunk_ranges_match_oracle(yuear):
+    rng = random.Random(8)
+    cases = [(10, 24570, 24576), (5000, 100, 24576), (30000, 0, 24576), (7, 10, 20), (1, 0, 5),
+             (2 ** 31 - 1, 0, 24576)]
+    cases += [(rng.randrange(1, 100000), rng.randrange(0, 24576), rng.randrange(5, 24577))
+              for _ in range(300)]
+    for frames, prefix, context in cases:
+        try:
+            want = text_ref.chunk_ranges(frames, prefix, context)
+        except ValueError:
+            with pytest.raises(ValueError, match="Empty codec or prefix leaves no acoustic"):
+                yuear.chunk_ranges(frames, prefix, context)
+            continue
+        if frames > 10 ** 6:  # the oracle's list is long; compare ends and count
+            got = yuear.chunk_ranges(frames, prefix, context)
+            assert (got[0], got[-1], len(got)) == (want[0], want[-1], len(want))
+            continue
+        assert yuear.chunk_ranges(frames, prefix, context) == want, (frames, prefix, context)
+    for frames, prefix in ((0, 10), (5, 24572), (5, 30000), (-3, 0)):
+        with pytest.raises(ValueError, match="Empty codec or prefix leaves no acoustic context"):
+            yuear.chunk_ranges(frames, prefix)

@@ -1,7 +1,7 @@
 // Text side of the request, host only: the checkpoint-native tiktoken BPE
 // (lyra::Tokenizer, protocol.hpp:5-16, protocol.mm:428-591) and the prompt
 // layout around the AR prefixes (instruction, SongRequest::text / validate,
-// token_prefixes, negative_prefix: protocol.mm:123-357).
+// token_prefixes, negative_prefix, chunk_ranges: protocol.mm:123-369).
 //
 // encode(text): strict UTF-8 -> code points -> NFC (the reference's
 // precomposedStringWithCanonicalMapping) -> pre-tokenizer pieces -> byte
@@ -734,6 +734,24 @@ yuear_status yuear_negative_prefix(const yuear_tokenizer *t, const yuear_song_re
       out.insert(out.end(), {yuear::kAbcEnd, yuear::kMusicStart});
     }
     yuear::give_ids(out, ids, n);
+  });
+}
+
+yuear_status yuear_chunk_ranges(int32_t frames, int32_t prefix_tokens, int32_t context,
+                                int32_t **bounds, int64_t *n, char **error_json) {
+  return yuear::guarded(error_json, [&] {
+    const int64_t available = int64_t(context) - prefix_tokens - 3;
+    if (frames < 1 || available < 2)
+      yuear::invalid("Empty codec or prefix leaves no acoustic context");
+    const int64_t size = std::min<int64_t>(available / 2, yuear::kContext);
+    std::vector<int32_t> out;
+    out.reserve(size_t((int64_t(frames) + size - 1) / size) * 2);
+    for (int64_t a = 0; a < frames; a += size) {
+      out.push_back(int32_t(a));
+      out.push_back(int32_t(std::min<int64_t>(a + size, frames)));
+    }
+    yuear::give_ids(out, bounds, n);
+    *n /= 2;
   });
 }
 

@@ -160,6 +160,8 @@ _SIGS = {
                                        _P(i32p), _P(C.c_int64), _P(C.c_void_p)]),
     "yuear_negative_prefix": (C.c_int, [C.c_void_p, _P(SongRequestC), i32p, C.c_int64,
                                         C.c_int32, _P(i32p), _P(C.c_int64), _P(C.c_void_p)]),
+    "yuear_chunk_ranges": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, _P(i32p), _P(C.c_int64),
+                                     _P(C.c_void_p)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -733,3 +735,13 @@ def token_prefixes(request, tokenizer, abc_ids=None):
 def negative_prefix(request, tokenizer, abc_ids=None):
     """negative_prefix (protocol.mm:341-357)."""
     return _prefix(lib.yuear_negative_prefix, tokenizer, request, abc_ids)
+
+
+def chunk_ranges(frames, prefix_tokens, context=24576):
+    """chunk_ranges (protocol.mm:358-369): [(a, b), ...] frame chunks."""
+    ptr, n, err = i32p(), C.c_int64(), C.c_void_p()
+    _check(lib.yuear_chunk_ranges(int(frames), int(prefix_tokens), int(context), C.byref(ptr),
+                                  C.byref(n), C.byref(err)), err)
+    flat = [ptr[i] for i in range(2 * n.value)]
+    lib.yuear_ids_free(ptr)
+    return list(zip(flat[0::2], flat[1::2]))
