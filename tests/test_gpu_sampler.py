@@ -68,6 +68,10 @@ CASES = [
     ("topp-flat", dict(temperature=1.0, top_k=5000, top_p=0.5), 1, 1.0, "full", "flat"),
     ("all-vocab", dict(temperature=1.3, top_k=100000, top_p=1.0), 1, 1.0, "full", "normal"),
     ("peaked", dict(temperature=1.0, top_k=100, top_p=0.95), 1, 1.0, "full", "peaked"),
+    # 257-512 survivors: the one-wave register sort at its largest size
+    ("topk-400", dict(temperature=1.0, top_k=400, top_p=0.9), 1, 1.0, "full", "normal"),
+    # 1025-4096 survivors: the LDS sort of the rows gathered after the first digit
+    ("topk-2000-cfg", dict(temperature=0.8, top_k=2000, top_p=0.8), 2, 1.5, "full", "normal"),
 ]
 
 
@@ -108,6 +112,34 @@ def test_sampler_penalty_and_min_tokens_semantic(engine_yue2, oracle):
         got = session.sample(sampling, seed, step, history=hist)
         want = oracle_token(oracle, logits, sampling, seed, step, hist, "semantic")
         assert got == want, (trial, got, want)
+    session.close()
+
+
+@pytest.mark.parametrize("top_k,top_p", [(100, 0.95), (20, 1.0), (5000, 0.9)])
+def test_sampler_end_row_both_penalised_and_masked(engine_yue2, oracle, top_k, top_p):
+    # the end token inside the penalty window while min_tokens still masks
+    # it: the row is special twice over (masked, then penalised: -inf either
+    # way) and must be replaced once in the scores and their counts
+    rng = np.random.default_rng(11 + top_k)
+    sampling = dict(temperature=1.0, top_p=top_p, top_k=top_k, repetition_penalty=1.2,
+                    penalty_window=50, min_tokens=200, max_tokens=9000)
+    session = engine_yue2.session(1, 64, "semantic")
+    n = session.vocab
+    for trial in range(12):
+        x = rng.normal(size=(1, n)) * 2
+        hist = [CODEC_OFFSET + int(t) for t in rng.integers(0, 40, size=60)]
+        for at in rng.integers(10, 60, size=1 + trial % 3):
+            hist[int(at)] = MUSIC_END
+        x[0, 0] += 8  # the end row would lead if it were not masked
+        logits = bf(x)
+        session.write_logits(logits)
+        step = 100 if trial % 3 else 250  # masked, masked, unmasked
+        seed = int(rng.integers(0, 2**62))
+        got = session.sample(sampling, seed, step, history=hist)
+        want = oracle_token(oracle, logits, sampling, seed, step, hist, "semantic")
+        assert got == want, (trial, got, want)
+        if step < 200:
+            assert got != MUSIC_END
     session.close()
 
 

@@ -11,12 +11,16 @@
 //     `penalty_window` emitted tokens, alpha = pow(p, count) from a host-built
 //     table (the lookup form of vendor fast.py:123-136).
 //  3. temperature 0: argmax (lowest index on ties).
-//  4. otherwise: temperature; exact k-th largest threshold by a 3-pass radix
-//     select on order-preserving keys (ties at the cut survive); ordered
-//     compaction of the survivors; for top_p < 1 a bitonic sort by (value
-//     desc, index asc), portable-exp softmax and the shifted-cumsum cut
-//     evaluated sequentially in that order; Gumbel-max draw with Philox
-//     uniforms u(seed, step, index).
+//  4. otherwise: temperature; exact k-th largest threshold by a radix select
+//     on order-preserving keys (ties at the cut survive): the first digit
+//     (13 bits) is counted while the scores are written and the rows at or
+//     above its cut are gathered into LDS; up to 256 of them are ordered by
+//     rank counting and the threshold read off that order, more go through
+//     the other two digits (11, 8 bits); for top_p < 1 the survivors sorted
+//     by (value desc, index asc) (rank counting, or a bitonic network beyond
+//     256), portable-exp softmax and the shifted-cumsum cut evaluated
+//     sequentially in that order (one wave stepping through lanes);
+//     Gumbel-max draw with Philox uniforms u(seed, step, index).
 #include <type_traits>
 
 #include "common.h"
@@ -29,22 +33,43 @@ namespace {
 constexpr int kT = 1024;        // threads
 constexpr int kWaves = kT / 64;
 constexpr int kSortLds = 4096;  // survivors sorted in LDS up to this count
+// Radix digits of the order keys: the top 13 bits (counted while the scores
+// are written), then 11, then 8; kBins covers the widest.
+constexpr int kShift0 = 19, kShift1 = 8;
+constexpr int kBins = 8192;
+// Rows whose first digit is at or above the cut digit, held in LDS for the
+// remaining digits when they fit (otherwise those passes read the scores).
+constexpr int kList = 4096;
+// Up to this many rows are ordered by rank counting instead of a network.
+constexpr int kRankSort = 256;
+static_assert(4 * kRankSort <= kT, "rank_sort counts with four threads per row");
+
+// A row as one sortable word: ascending order is (score desc, index asc).
+__device__ __forceinline__ uint64_t row_word(uint32_t key, uint32_t index) {
+  return (uint64_t(~key) << 32) | index;
+}
 
 struct Shared {
   union {
     struct {
-      uint32_t key[kSortLds];
+      uint32_t key[kSortLds];  // ~order key: ascending = score descending
       uint32_t idx[kSortLds];
     } sort;
     uint32_t bits[2 * kSortLds];  // special-index bitmap (up to 262144 rows)
   } u;
-  uint32_t hist[2048];
+  uint64_t list[kList];  // row_word of the rows gathered after the first digit
+  union {
+    uint32_t hist[kBins];
+    uint64_t stage[kBins / 2];  // survivors' row words, once the digits are done
+  };
   int wave_tmp[kWaves];
   float wave_val[kWaves];
   int wave_idx[kWaves];
   int pen_loc[128];
   int bcast[4];
   int count;
+  int n_surv;
+  int end_penalised;  // the masked end row is also a penalised row
   float prob[kSortLds];
   uint8_t keep[kSortLds];
 };
@@ -151,6 +176,78 @@ __device__ void bitonic(uint32_t *key, uint32_t *idx, int n) {
   }
 }
 
+// The bin of sh.hist that holds the krem-th largest counted key (1-based,
+// krem >= 1 and at most the number counted), the rank left inside that bin
+// and the bin's count; every thread receives all three. Thread t owns the
+// kBins / kT consecutive bins from t * (kBins / kT).
+__device__ void find_cut(Shared &sh, int krem, int *bin, int *rem, int *in_bin) {
+  constexpr int B = kBins / kT;
+  const int t = threadIdx.x;
+  int h[B], s = 0;
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    h[b] = int(sh.hist[t * B + b]);
+    s += h[b];
+  }
+  int total;
+  const int incl = block_scan(s, sh, &total);
+  int acc = total - incl;  // keys in the bins above this thread's
+#pragma unroll
+  for (int b = B - 1; b >= 0; --b) {
+    if (acc < krem && krem <= acc + h[b]) {
+      sh.bcast[0] = t * B + b;
+      sh.bcast[1] = krem - acc;
+      sh.bcast[2] = h[b];
+    }
+    acc += h[b];
+  }
+  __syncthreads();
+  *bin = sh.bcast[0];
+  *rem = sh.bcast[1];
+  *in_bin = sh.bcast[2];
+  __syncthreads();
+}
+
+// Slot of this lane in a list grown by whole waves: the lanes whose `pred`
+// holds take consecutive slots from *counter (one LDS atomic per wave);
+// -1 for the others. Lanes of a wave may have left the loop around it.
+__device__ __forceinline__ int wave_append(bool pred, int *counter) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0)
+    return -1;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  int base = 0;
+  if ((threadIdx.x & 63) == leader)
+    base = atomicAdd(counter, __popcll(m));
+  base = __builtin_amdgcn_readlane(base, leader);
+  const int below =
+      __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
+  return pred ? base + below : -1;
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Ascending sort of m <= kRankSort distinct row words by rank counting:
+// four threads count the words below each one (LDS broadcast reads, no
+// barriers between steps) and the word goes to that position of key/idx.
+__device__ void rank_sort(const uint64_t *src, int m, uint32_t *key, uint32_t *idx) {
+  const int e = threadIdx.x >> 2, q = threadIdx.x & 3;
+  const uint64_t mine = e < m ? src[e] : 0;
+  int below = 0;
+  if (e < m)
+    for (int u = q; u < m; u += 4)
+      below += src[u] < mine;
+  below += __shfl_xor(below, 1, 64);
+  below += __shfl_xor(below, 2, 64);
+  if (e < m && q == 0) {
+    key[below] = uint32_t(mine >> 32);
+    idx[below] = uint32_t(mine);
+  }
+  __syncthreads();
+}
+
 struct Ctx {
   const SamplerParams &p;
   bool legacy, cfg;
@@ -238,6 +335,14 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
   const int nw = (n + 31) >> 5;
   for (int i = tid; i < nw; i += kT)
     sh.u.bits[i] = 0;
+  if (!greedy)
+    for (int i = tid; i < kBins; i += kT)
+      sh.hist[i] = 0;
+  if (tid == 0) {
+    sh.count = 0;
+    sh.n_surv = 0;
+    sh.end_penalised = 0;
+  }
   const int hlen = p.hist_len < 0 ? step : p.hist_len;
   const int wlen = p.alphas && p.penalty_window > 0 ? min(hlen, p.penalty_window) : 0;
   if (tid < wlen)
@@ -256,6 +361,8 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
       atomicOr(&sh.u.bits[loc >> 5], 1u << (loc & 31));
     else
       pen_count = 0;
+    if (pen_count > 0 && loc == end && end_masked)
+      sh.end_penalised = 1;
   }
   if (tid == 0 && end_masked)
     atomicOr(&sh.u.bits[end >> 5], 1u << (end & 31));
@@ -348,151 +455,281 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
     if (local == 0x7fffffff) local = 0;
   } else {
     float *sc = p.scratch;
-    // 4a. scores with penalty and temperature (sampling.cpp:44-81)
-    for (int c = tid; c < n8; c += kT) {
-      float v[8];
-      cx.chunk(c, v);
+    uint32_t *surv = p.scratch_u;  // [n] survivor indices outside LDS
+    const int k = min(p.top_k, n);
+    const bool select = k < n;  // otherwise every row survives
+    // 4a. scores with penalty and temperature (sampling.cpp:44-81), counted
+    // by their first radix digit in the same pass (k-th largest below)
+    constexpr int kU = 4;  // chunks in flight per thread
+    for (int c0 = tid; c0 < n8; c0 += kU * kT) {
+      float v[kU][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        v[e] = cx.temp(v[e]);
-      reinterpret_cast<float4 *>(sc)[2 * c] = make_float4(v[0], v[1], v[2], v[3]);
-      reinterpret_cast<float4 *>(sc)[2 * c + 1] = make_float4(v[4], v[5], v[6], v[7]);
+      for (int u = 0; u < kU; ++u)
+        cx.chunk(min(c0 + u * kT, n8 - 1), v[u]);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int c = c0 + u * kT;
+        if (c < n8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            v[u][e] = cx.temp(v[u][e]);
+            if (select)
+              atomicAdd(&sh.hist[order_key(v[u][e]) >> kShift0], 1u);
+          }
+          reinterpret_cast<float4 *>(sc)[2 * c] =
+              make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          reinterpret_cast<float4 *>(sc)[2 * c + 1] =
+              make_float4(v[u][4], v[u][5], v[u][6], v[u][7]);
+        }
+      }
     }
-    for (int i = 8 * n8 + tid; i < n; i += kT)
-      sc[i] = cx.temp(cx.one(i));
+    for (int i = 8 * n8 + tid; i < n; i += kT) {
+      const float v = cx.temp(cx.one(i));
+      sc[i] = v;
+      if (select)
+        atomicAdd(&sh.hist[order_key(v) >> kShift0], 1u);
+    }
     __syncthreads();
+    // special rows: the final score replaces the plain one, in the scores
+    // and in the count
+    auto patch = [&](int loc, float s) {
+      if (select) {
+        atomicSub(&sh.hist[order_key(cx.temp(cx.one(loc))) >> kShift0], 1u);
+        atomicAdd(&sh.hist[order_key(s) >> kShift0], 1u);
+      }
+      sc[loc] = s;
+    };
     if (pen_count > 0) {
       const int loc = sh.pen_loc[tid];
-      sc[loc] = cx.temp(special_score(loc, pen_count));
+      patch(loc, cx.temp(special_score(loc, pen_count)));
     }
-    if (tid == 0 && end_masked)
-      sc[end] = ninf;
+    if (tid == 0 && end_masked && !sh.end_penalised)
+      patch(end, ninf);
     __syncthreads();
-    // 4b. k-th largest threshold (sampling.cpp:82-84): 3-pass radix select
-    const int k = min(p.top_k, n);
+
+    // 4b. k-th largest threshold (sampling.cpp:82-84) on order-preserving
+    // keys. The rows at or above the cut first digit (all of the top k) are
+    // gathered into LDS when they fit; up to kRankSort of them are ordered at
+    // once and the k-th largest read off that order, more go through the
+    // other two digits (11, 8 bits), and without room every pass reads the
+    // scores instead.
     const int n4 = n >> 2;
-    uint32_t thr_key = 0;
-    if (k < n) {
-      uint32_t prefix = 0, pmask = 0;
-      int krem = k;
-      const int shifts[3] = {21, 10, 0};
-      const int widths[3] = {11, 11, 10};
-      for (int pass = 0; pass < 3; ++pass) {
-        const int shift = shifts[pass];
-        const uint32_t dmask = (1u << widths[pass]) - 1u;
-        for (int i = tid; i < 2048; i += kT)
-          sh.hist[i] = 0;
-        __syncthreads();
-        for (int c = tid; c < n4; c += kT) {
-          const float4 f = reinterpret_cast<const float4 *>(sc)[c];
-          const float fv[4] = {f.x, f.y, f.z, f.w};
+    uint32_t *key = sh.u.sort.key, *idx = sh.u.sort.idx;  // sorted survivors
+    bool in_list = false;  // survivors are in sh.stage (else in surv)
+    bool sorted = false;   // key/idx hold the n_s survivors in order
+    int n_s = 0;
+    if (select) {
+      int digit, krem, in_digit;
+      find_cut(sh, k, &digit, &krem, &in_digit);
+      uint32_t prefix = uint32_t(digit) << kShift0, pmask = ~0u << kShift0;
+      const int L = k - krem + in_digit;  // rows above the cut digit, and in it
+      in_list = L <= kList;
+      if (in_list) {
+        for (int c0 = tid; c0 < n4; c0 += kU * kT) {
+          float4 f[kU];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t key = order_key(fv[e]);
-            if ((key & pmask) == prefix)
-              atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+          for (int u = 0; u < kU; ++u)
+            f[u] = reinterpret_cast<const float4 *>(sc)[min(c0 + u * kT, n4 - 1)];
+#pragma unroll
+          for (int u = 0; u < kU; ++u) {
+            const int c = c0 + u * kT;
+            const float fv[4] = {f[u].x, f[u].y, f[u].z, f[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t key_e = order_key(fv[e]);
+              const int slot = wave_append(c < n4 && key_e >= prefix, &sh.count);
+              if (slot >= 0 && slot < kList)
+                sh.list[slot] = row_word(key_e, uint32_t(4 * c + e));
+            }
           }
         }
         for (int i = 4 * n4 + tid; i < n; i += kT) {
-          const uint32_t key = order_key(sc[i]);
-          if ((key & pmask) == prefix)
-            atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
+          const uint32_t key_i = order_key(sc[i]);
+          const int slot = wave_append(key_i >= prefix, &sh.count);
+          if (slot >= 0 && slot < kList)
+            sh.list[slot] = row_word(key_i, uint32_t(i));
         }
-        __syncthreads();
-        // thread t owns bins 2t (low) and 2t+1 (high); count strictly above
-        const int h0 = int(sh.hist[2 * tid]), h1 = int(sh.hist[2 * tid + 1]);
-        int total;
-        const int incl = block_scan(h0 + h1, sh, &total);
-        const int above = total - incl;  // bins > 2t+1
-        if (above < krem && krem <= above + h1) {
-          sh.bcast[0] = 2 * tid + 1;
-          sh.bcast[1] = krem - above;
-        } else if (above + h1 < krem && krem <= above + h1 + h0) {
-          sh.bcast[0] = 2 * tid;
-          sh.bcast[1] = krem - above - h1;
-        }
-        __syncthreads();
-        prefix |= uint32_t(sh.bcast[0]) << shift;
-        pmask |= dmask << shift;
-        krem = sh.bcast[1];
         __syncthreads();
       }
-      thr_key = prefix;
-    }
-    // 4c. survivors (score >= threshold, ties kept), compacted in any order:
-    // the nucleus sort and the draw's index tie-break restore determinism
-    if (tid == 0) sh.count = 0;
-    __syncthreads();
-    uint32_t *surv = p.scratch_u;  // [n] survivor indices
-    for (int c = tid; c < n4; c += kT) {
-      const float4 f = reinterpret_cast<const float4 *>(sc)[c];
-      const float fv[4] = {f.x, f.y, f.z, f.w};
+      if (in_list && L <= kRankSort) {
+        rank_sort(sh.list, L, key, idx);
+        // survivors: the sorted prefix down to the k-th largest score, with
+        // every row tied with it
+        const uint32_t cut = key[k - 1];
+        for (int r = tid; r < L; r += kT)
+          if (key[r] <= cut)
+            atomicMax(&sh.n_surv, r + 1);
+        sorted = true;
+      } else {
+        for (int pass = 1; pass < 3; ++pass) {
+          const int shift = pass == 1 ? kShift1 : 0;
+          const uint32_t dmask = pass == 1 ? 0x7ffu : 0xffu;
+          for (int i = tid; i < kBins; i += kT)
+            sh.hist[i] = 0;
+          __syncthreads();
+          if (in_list) {
+            for (int i = tid; i < L; i += kT) {
+              const uint32_t key_i = ~uint32_t(sh.list[i] >> 32);
+              if ((key_i & pmask) == prefix)
+                atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
+            }
+          } else {
+            for (int c = tid; c < n4; c += kT) {
+              const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+              const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (order_key(fv[e]) >= thr_key)
-          surv[atomicAdd(&sh.count, 1)] = uint32_t(4 * c + e);
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t key_e = order_key(fv[e]);
+                if ((key_e & pmask) == prefix)
+                  atomicAdd(&sh.hist[(key_e >> shift) & dmask], 1u);
+              }
+            }
+            for (int i = 4 * n4 + tid; i < n; i += kT) {
+              const uint32_t key_i = order_key(sc[i]);
+              if ((key_i & pmask) == prefix)
+                atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
+            }
+          }
+          __syncthreads();
+          int d, in_d;
+          find_cut(sh, krem, &d, &krem, &in_d);
+          prefix |= uint32_t(d) << shift;
+          pmask |= dmask << shift;
+        }
+        // 4c. survivors (key >= prefix, ties at the cut kept), compacted in
+        // any order: the nucleus sort and the draw's index tie-break restore
+        // determinism
+        if (in_list) {
+          for (int i = tid; i < L; i += kT) {
+            const uint64_t w = sh.list[i];
+            const int slot = wave_append(~uint32_t(w >> 32) >= prefix, &sh.n_surv);
+            if (slot >= 0)
+              sh.stage[slot] = w;
+          }
+        } else {
+          for (int c = tid; c < n4; c += kT) {
+            const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+            const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (order_key(fv[e]) >= prefix)
+                surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(4 * c + e);
+          }
+          for (int i = 4 * n4 + tid; i < n; i += kT)
+            if (order_key(sc[i]) >= prefix)
+              surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(i);
+        }
+      }
+    } else {  // every row survives
+      for (int i = tid; i < n; i += kT)
+        surv[i] = uint32_t(i);
+      if (tid == 0)
+        sh.n_surv = n;
     }
-    for (int i = 4 * n4 + tid; i < n; i += kT)
-      if (order_key(sc[i]) >= thr_key)
-        surv[atomicAdd(&sh.count, 1)] = uint32_t(i);
     __syncthreads();
-    const int n_s = sh.count;
+    n_s = sh.n_surv;
 
     float bv = ninf;
     int bi = 0x7fffffff;
     if (p.top_p >= 1.0f) {
       // 4e. draw over the survivors (Gumbel-max)
       for (int r = tid; r < n_s; r += kT) {
-        const int i = int(surv[r]);
-        const float v = sc[i];
+        int i;
+        float v;
+        if (sorted) {
+          i = int(idx[r]);
+          v = key_value(~key[r]);
+        } else if (in_list) {
+          const uint64_t w = sh.stage[r];
+          i = int(uint32_t(w));
+          v = key_value(~uint32_t(w >> 32));
+        } else {
+          i = int(surv[r]);
+          v = sc[i];
+        }
         if (!(v > ninf)) continue;
-        const float key = v + gumbel(draw_uniform(p.seed, step, i));
-        if (better(key, i, bv, bi)) {
-          bv = key;
+        const float gk = v + gumbel(draw_uniform(p.seed, step, i));
+        if (better(gk, i, bv, bi)) {
+          bv = gk;
           bi = i;
         }
       }
     } else {
       // 4d. nucleus over survivors sorted by (value desc, index asc)
-      int P = 1;
-      while (P < n_s) P <<= 1;
-      const bool in_lds = P <= kSortLds;
-      uint32_t *key = in_lds ? sh.u.sort.key : p.scratch_u + n;
-      uint32_t *idx = in_lds ? sh.u.sort.idx : p.scratch_u + n + P;
-      __syncthreads();  // the bitmap shares storage with the LDS sort arrays
-      for (int r = tid; r < P; r += kT) {
-        if (r < n_s) {
-          const int i = int(surv[r]);
-          key[r] = ~order_key(sc[i]);
-          idx[r] = uint32_t(i);
-        } else {
-          key[r] = 0xffffffffu;
-          idx[r] = 0x7fffffffu;
+      bool in_lds = true;
+      if (!sorted && n_s <= kRankSort) {
+        if (!in_list) {
+          for (int r = tid; r < n_s; r += kT) {
+            const uint32_t i = surv[r];
+            sh.stage[r] = row_word(order_key(sc[i]), i);
+          }
+          __syncthreads();
         }
+        rank_sort(sh.stage, n_s, key, idx);
+      } else if (!sorted) {
+        int P = 1;
+        while (P < n_s) P <<= 1;
+        in_lds = P <= kSortLds;
+        if (!in_lds) {
+          key = p.scratch_u + n;
+          idx = p.scratch_u + n + P;
+        }
+        for (int r = tid; r < P; r += kT) {
+          if (r >= n_s) {
+            key[r] = 0xffffffffu;
+            idx[r] = 0x7fffffffu;
+          } else if (in_list) {
+            const uint64_t w = sh.stage[r];
+            key[r] = uint32_t(w >> 32);
+            idx[r] = uint32_t(w);
+          } else {
+            const uint32_t i = surv[r];
+            key[r] = ~order_key(sc[i]);
+            idx[r] = i;
+          }
+        }
+        __syncthreads();
+        bitonic(key, idx, P);
       }
-      __syncthreads();
-      bitonic(key, idx, P);
       float *prob = in_lds ? sh.prob : reinterpret_cast<float *>(surv);
       uint8_t *keep = in_lds ? sh.keep : nullptr;
-      const float m = sc[idx[0]];
+      const float m = key_value(~key[0]);
       for (int r = tid; r < n_s; r += kT)
-        prob[r] = m == ninf ? 0.f : portable_exp(sc[idx[r]] - m);
+        prob[r] = m == ninf ? 0.f : portable_exp(key_value(~key[r]) - m);
       __syncthreads();
-      if (tid == 0) {
-        float total = 0.f;  // sequential sum in sorted order
-        for (int r = 0; r < n_s; ++r)
-          total += prob[r];
+      // sequential sums in sorted order, on one wave: 64 values at a time
+      // are loaded and divided in parallel and the running sums step through
+      // them lane by lane. Zeros after the last survivor leave both sums as
+      // they are.
+      if (tid < 64) {
+        const int lane = tid;
+        float total = 0.f;
+        for (int r0 = 0; r0 < n_s; r0 += 64) {
+          const float pv = r0 + lane < n_s ? prob[r0 + lane] : 0.f;
+#pragma unroll
+          for (int j = 0; j < 64; ++j)
+            total += lane_value(pv, j);
+        }
         const int minimum = cx.legacy ? 3 : 1;
         float cum = 0.f;
-        for (int r = 0; r < n_s; ++r) {
-          const float pr = cx.legacy ? rbf(prob[r] / total) : prob[r] / total;
-          cum = cx.cast(cum + pr);
-          const float pre = cx.cast(cum - pr);
-          const bool removed = pre > p.top_p && r >= minimum;
-          if (keep)
-            keep[r] = !removed;
-          else
-            prob[r] = removed ? 0.f : 1.f;
+        for (int r0 = 0; r0 < n_s; r0 += 64) {
+          const int r = r0 + lane;
+          const float pv = r < n_s ? prob[r] : 0.f;
+          const float pr = cx.legacy ? rbf(pv / total) : pv / total;
+          float cum_r = 0.f;
+#pragma unroll
+          for (int j = 0; j < 64; ++j) {
+            cum = cx.cast(cum + lane_value(pr, j));
+            cum_r = lane == j ? cum : cum_r;
+          }
+          if (r < n_s) {
+            const float pre = cx.cast(cum_r - pr);
+            const bool removed = pre > p.top_p && r >= minimum;
+            if (keep)
+              keep[r] = !removed;
+            else
+              prob[r] = removed ? 0.f : 1.f;
+          }
         }
       }
       __syncthreads();
@@ -500,7 +737,7 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
         const bool kept = keep ? keep[r] != 0 : prob[r] != 0.f;
         if (!kept) continue;
         const int i = int(idx[r]);
-        const float v = sc[i];
+        const float v = key_value(~key[r]);
         if (!(v > ninf)) continue;
         const float gk = v + gumbel(draw_uniform(p.seed, step, i));
         if (better(gk, i, bv, bi)) {
