@@ -272,6 +272,7 @@ struct yuear_session {
   float *scratch = nullptr, *alphas = nullptr;
   uint32_t *scratch_u = nullptr;
   int32_t *sstate = nullptr, *history = nullptr;
+  int32_t *sampler_sync = nullptr;  // split sampler counters, zero between launches
   int history_cap = 0;       // history entries per branch set
   int scratch_u_stride = 0;
   // prefill scratch
@@ -643,6 +644,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.scratch = S.alloc<float>(size_t(S.phase.size) * sets);
   S.scratch_u = S.alloc<uint32_t>(size_t(S.scratch_u_stride) * sets);
   S.alphas = S.alloc<float>(128);
+  S.sampler_sync = S.alloc<int32_t>(2);
+  HIPC(hipMemsetAsync(S.sampler_sync, 0, 2 * sizeof(int32_t), S.stream));
   S.sstate = S.alloc<int32_t>(2 * sets);
   S.history_cap = kContext;
   S.history = S.alloc<int32_t>(size_t(S.history_cap) * sets);
@@ -1037,6 +1040,7 @@ SamplerParams sampler_params(yuear_session &S, const yuear_sampling &s, uint64_t
   p.tokens_out = S.tok;
   p.scratch = S.scratch;
   p.scratch_u = S.scratch_u;
+  p.sync = S.sampler_sync;  // the shared-draw case may spread over workgroups
   if (S.B > 2) {  // batched sequences: each branch is its own request
     p.independent = 1;
     p.history_stride = S.history_cap;

@@ -161,7 +161,13 @@ struct SamplerParams {
   // all branches (a request, or a CFG pair).
   int independent = 0;
   int history_stride = 0, scratch_stride = 0, scratch_u_stride = 0;
+  // [2] arrival and candidate counters, zero between launches: with them a
+  // shared draw (greedy, or top k up to 128) over more than 8192 rows is
+  // spread over one workgroup per ~8192 rows; null keeps one workgroup.
+  int32_t *sync = nullptr;
+  int split_rows = 0;  // set by launch_sampler
 };
+// scratch_u must hold n 8-byte candidate words (2n entries) when sync is set.
 hipError_t launch_sampler(const SamplerParams &p, hipStream_t s);
 
 // ---- prefill ----

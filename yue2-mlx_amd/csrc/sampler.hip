@@ -21,6 +21,7 @@
 //     256), portable-exp softmax and the shifted-cumsum cut evaluated
 //     sequentially in that order (one wave stepping through lanes);
 //     Gumbel-max draw with Philox uniforms u(seed, step, index).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -42,6 +43,10 @@ constexpr int kBins = 8192;
 constexpr int kList = 4096;
 // Up to this many rows are ordered by rank counting instead of a network.
 constexpr int kRankSort = 256;
+// The split kernel samples top k up to this (greedy at any k), with at
+// most kMaxGroups workgroups (rows up to 262144 in groups of 8192).
+constexpr int kSplitMaxTopK = 128;
+constexpr int kMaxGroups = 32;
 static_assert(4 * kRankSort <= kT, "rank_sort counts with four threads per row");
 
 // A row as one sortable word: ascending order is (score desc, index asc).
@@ -57,7 +62,10 @@ struct Shared {
     } sort;
     uint32_t bits[2 * kSortLds];  // special-index bitmap (up to 262144 rows)
   } u;
-  uint64_t list[kList];  // row_word of the rows gathered after the first digit
+  union {
+    uint64_t list[kList];  // row words of the rows gathered after the first digit
+    uint32_t slice[2 * kList];  // order keys of a split workgroup's rows
+  };
   union {
     uint32_t hist[kBins];
     uint64_t stage[kBins / 2];  // survivors' row words, once the digits are done
@@ -70,6 +78,7 @@ struct Shared {
   int count;
   int n_surv;
   int end_penalised;  // the masked end row is also a penalised row
+  int is_last;        // split kernel: this workgroup arrived last
   float prob[kSortLds];
   uint8_t keep[kSortLds];
 };
@@ -178,34 +187,60 @@ __device__ void bitonic(uint32_t *key, uint32_t *idx, int n) {
 
 // The bin of sh.hist that holds the krem-th largest counted key (1-based,
 // krem >= 1 and at most the number counted), the rank left inside that bin
-// and the bin's count; every thread receives all three. Thread t owns the
-// kBins / kT consecutive bins from t * (kBins / kT).
+// and the bin's count; every thread receives all three. One wave: lane l
+// sums bins [128 l, 128 l + 128) (reading its 32 16-byte pieces in a
+// lane-rotated order, so a wave's reads spread over the LDS banks), a
+// suffix scan over lanes finds the 128-bin group, then the group's bins,
+// two per lane, the bin. Callers separate consecutive calls by a barrier
+// (the result goes through sh.bcast).
 __device__ void find_cut(Shared &sh, int krem, int *bin, int *rem, int *in_bin) {
-  constexpr int B = kBins / kT;
-  const int t = threadIdx.x;
-  int h[B], s = 0;
-#pragma unroll
-  for (int b = 0; b < B; ++b) {
-    h[b] = int(sh.hist[t * B + b]);
-    s += h[b];
-  }
-  int total;
-  const int incl = block_scan(s, sh, &total);
-  int acc = total - incl;  // keys in the bins above this thread's
-#pragma unroll
-  for (int b = B - 1; b >= 0; --b) {
-    if (acc < krem && krem <= acc + h[b]) {
-      sh.bcast[0] = t * B + b;
-      sh.bcast[1] = krem - acc;
-      sh.bcast[2] = h[b];
+  static_assert(kBins == 64 * 128, "one wave, 128 bins per lane");
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const u32x4 *h4 = reinterpret_cast<const u32x4 *>(sh.hist);
+    int s = 0;
+#pragma unroll 8
+    for (int j = 0; j < 32; ++j) {
+      const u32x4 v = h4[lane * 32 + ((j + lane) & 31)];
+      s += int(v.x + v.y + v.z + v.w);
     }
-    acc += h[b];
+    int suf = s;  // keys in this lane's group and the groups above it
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_down(suf, o, 64);
+      if (lane + o < 64) suf += t;
+    }
+    const uint64_t hit = __ballot(suf - s < krem && krem <= suf);
+    const int g = hit ? __ffsll((unsigned long long)hit) - 1 : 0;  // one lane holds krem
+    const int kg = krem - __builtin_amdgcn_readlane(suf - s, g);
+    const int b0 = g * 128 + 2 * lane;
+    const int c0 = int(sh.hist[b0]), c1 = int(sh.hist[b0 + 1]);
+    int suf2 = c0 + c1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_down(suf2, o, 64);
+      if (lane + o < 64) suf2 += t;
+    }
+    const int above = suf2 - c0 - c1;  // keys in the group's bins above b0 + 1
+    if (lane == 0) {  // overwritten below by the lane holding the bin
+      sh.bcast[0] = 0;
+      sh.bcast[1] = 1;
+      sh.bcast[2] = 0;
+    }
+    if (above < kg && kg <= above + c1) {
+      sh.bcast[0] = b0 + 1;
+      sh.bcast[1] = kg - above;
+      sh.bcast[2] = c1;
+    } else if (above + c1 < kg && kg <= above + c1 + c0) {
+      sh.bcast[0] = b0;
+      sh.bcast[1] = kg - above - c1;
+      sh.bcast[2] = c0;
+    }
   }
   __syncthreads();
   *bin = sh.bcast[0];
   *rem = sh.bcast[1];
   *in_bin = sh.bcast[2];
-  __syncthreads();
 }
 
 // Slot of this lane in a list grown by whole waves: the lanes whose `pred`
@@ -236,9 +271,14 @@ __device__ void rank_sort(const uint64_t *src, int m, uint32_t *key, uint32_t *i
   const int e = threadIdx.x >> 2, q = threadIdx.x & 3;
   const uint64_t mine = e < m ? src[e] : 0;
   int below = 0;
-  if (e < m)
-    for (int u = q; u < m; u += 4)
+  if (e < m) {
+    int u = q;
+    for (; u + 12 < m; u += 16)  // four independent reads in flight
+      below += int(src[u] < mine) + int(src[u + 4] < mine) + int(src[u + 8] < mine) +
+               int(src[u + 12] < mine);
+    for (; u < m; u += 4)
       below += src[u] < mine;
+  }
   below += __shfl_xor(below, 1, 64);
   below += __shfl_xor(below, 2, 64);
   if (e < m && q == 0) {
@@ -257,6 +297,10 @@ struct Ctx {
   // sampling.cpp:100-115), before penalty and temperature.
   __device__ void chunk(int c, float *out) const {
     const u32x4 a = reinterpret_cast<const u32x4 *>(p.logits)[c];
+    merge(a, cfg ? reinterpret_cast<const u32x4 *>(p.logits + p.ls)[c] : a, out);
+  }
+  // The same from the chunk's loaded words (u: the unconditional branch's).
+  __device__ void merge(const u32x4 a, const u32x4 u, float *out) const {
     const uint32_t av[4] = {a.x, a.y, a.z, a.w};
     if (!cfg) {
 #pragma unroll
@@ -266,7 +310,6 @@ struct Ctx {
       }
       return;
     }
-    const u32x4 u = reinterpret_cast<const u32x4 *>(p.logits + p.ls)[c];
     const uint32_t uv[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -292,26 +335,282 @@ __device__ __forceinline__ bool special(const Shared &sh, int i) {
   return (sh.u.bits[i >> 5] >> (i & 31)) & 1u;
 }
 
-__global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
-  __shared__ Shared sh;
-  SamplerParams p = p0;
-  if (p0.independent) {  // workgroup b: branch b on its own, as a 1-branch request
-    const int b = blockIdx.x;
-    p.logits += size_t(b) * p0.ls;
-    p.branches = 1;
-    p.state += 2 * b;
-    p.history += size_t(b) * p0.history_stride;
-    p.tokens_out += b;
-    p.scratch += size_t(b) * p0.scratch_stride;
-    p.scratch_u += size_t(b) * p0.scratch_u_stride;
-    p.seed += uint64_t(b);
+// Special rows among [lo, lo + span): the end row while masked and the
+// distinct local ids of the penalty window (sampling.cpp:51-75), marked in
+// the LDS bitmap at bit (row - lo). Returns, for the thread that holds the
+// first occurrence of a penalised row in the window (sh.pen_loc[tid]), the
+// row's count in the window, else 0. Also clears the histogram (when asked),
+// the list counters and end_penalised.
+__device__ __forceinline__ int mark_specials(const SamplerParams &p, Shared &sh, int step, int end,
+                             bool end_masked, int lo, int span, bool clear_hist) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < (span + 31) >> 5; i += kT)
+    sh.u.bits[i] = 0;
+  if (clear_hist)
+    for (int i = tid; i < kBins; i += kT)
+      sh.hist[i] = 0;
+  if (tid == 0) {
+    sh.count = 0;
+    sh.n_surv = 0;
+    sh.end_penalised = 0;
   }
+  const int hlen = p.hist_len < 0 ? step : p.hist_len;
+  const int wlen = p.alphas && p.penalty_window > 0 ? min(hlen, p.penalty_window) : 0;
+  if (tid < wlen)
+    sh.pen_loc[tid] = local_of(p.history[hlen - wlen + tid], p.phase, p.vocab);
+  __syncthreads();
+  int pen_count = 0;
+  if (tid < wlen) {
+    const int loc = sh.pen_loc[tid];
+    bool first = loc >= 0 && loc < p.n;
+    for (int t = 0; t < wlen; ++t)
+      if (sh.pen_loc[t] == loc) {
+        ++pen_count;
+        if (t < tid) first = false;
+      }
+    if (!first)
+      pen_count = 0;
+    if (pen_count > 0 && loc >= lo && loc < lo + span)
+      atomicOr(&sh.u.bits[(loc - lo) >> 5], 1u << ((loc - lo) & 31));
+    if (pen_count > 0 && loc == end && end_masked)
+      sh.end_penalised = 1;
+  }
+  if (tid == 0 && end_masked && end >= lo && end < lo + span)
+    atomicOr(&sh.u.bits[(end - lo) >> 5], 1u << ((end - lo) & 31));
+  __syncthreads();
+  return pen_count;
+}
+
+// Full score of a special row: mask, then penalty (a masked -inf stays
+// -inf); before temperature.
+__device__ __forceinline__ float special_score(const SamplerParams &p, const Ctx &cx, int loc,
+                                               int count, int end, bool end_masked) {
+  float v = cx.one(loc);
+  if (loc == end && end_masked)
+    v = cx.ninf;
+  if (count > 0) {
+    const float a = p.alphas[count];
+    v = v < 0.f ? cx.cast(v * a) : cx.cast(v / a);
+  }
+  return v;
+}
+
+// Survivors from rows held in sh.list[0, L): every row of the top k is
+// there, `top` of the rows have their first digit at or above the cut
+// (prefix under pmask) and the k-th largest score is the krem-th largest of
+// that digit. Up to kRankSort such rows are ordered at once (the list
+// itself when top == L, else gathered into sh.stage) and the survivors are
+// the sorted prefix down to the k-th largest with its ties: returns true,
+// survivors in key/idx. More rows go through the other two digits and the
+// survivors are left unsorted in sh.stage: returns false. sh.n_surv holds the
+// count after a barrier. sh.count must be 0.
+__device__ __forceinline__ bool select_in_list(Shared &sh, int L, int top, int k, uint32_t prefix,
+                               uint32_t pmask, int krem) {
+  const int tid = threadIdx.x;
+  uint32_t *key = sh.u.sort.key, *idx = sh.u.sort.idx;
+  if (top <= kRankSort) {
+    const uint64_t *src = sh.list;
+    if (top < L) {
+      for (int i = tid; i < L; i += kT) {
+        const uint64_t w = sh.list[i];
+        const int slot = wave_append(~uint32_t(w >> 32) >= prefix, &sh.count);
+        if (slot >= 0 && slot < kRankSort)
+          sh.stage[slot] = w;
+      }
+      __syncthreads();
+      src = sh.stage;
+    }
+    rank_sort(src, top, key, idx);
+    const uint32_t cut = key[k - 1];
+    for (int r = tid; r < top; r += kT)
+      if (key[r] <= cut)
+        atomicMax(&sh.n_surv, r + 1);
+    return true;
+  }
+  for (int pass = 1; pass < 3; ++pass) {
+    const int shift = pass == 1 ? kShift1 : 0;
+    const uint32_t dmask = pass == 1 ? 0x7ffu : 0xffu;
+    for (int i = tid; i < kBins; i += kT)
+      sh.hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < L; i += kT) {
+      const uint32_t key_i = ~uint32_t(sh.list[i] >> 32);
+      if ((key_i & pmask) == prefix)
+        atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    int d, in_d;
+    find_cut(sh, krem, &d, &krem, &in_d);
+    prefix |= uint32_t(d) << shift;
+    pmask |= dmask << shift;
+  }
+  // survivors (key >= prefix, ties at the cut kept), in any order: the
+  // nucleus sort and the draw's index tie-break restore determinism
+  for (int i = tid; i < L; i += kT) {
+    const uint64_t w = sh.list[i];
+    const int slot = wave_append(~uint32_t(w >> 32) >= prefix, &sh.n_surv);
+    if (slot >= 0 && slot < kBins / 2)
+      sh.stage[slot] = w;
+  }
+  return false;
+}
+
+// 4d/4e. The draw among the n_s survivors: sorted in the LDS key/idx
+// arrays (sorted), unsorted in sh.stage (in_stage), or unsorted in
+// surv = p.scratch_u with their scores in p.scratch.
+__device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh, const Ctx &cx, int step,
+                              int n_s, bool sorted, bool in_stage) {
+  const int tid = threadIdx.x, n = p.n;
+  const float ninf = cx.ninf;
+  const float *sc = p.scratch;
+  uint32_t *surv = p.scratch_u;
+  uint32_t *key = sh.u.sort.key, *idx = sh.u.sort.idx;
+  float bv = ninf;
+  int bi = 0x7fffffff;
+  if (p.top_p >= 1.0f) {
+    // 4e. draw over the survivors (Gumbel-max)
+    for (int r = tid; r < n_s; r += kT) {
+      int i;
+      float v;
+      if (sorted) {
+        i = int(idx[r]);
+        v = key_value(~key[r]);
+      } else if (in_stage) {
+        const uint64_t w = sh.stage[r];
+        i = int(uint32_t(w));
+        v = key_value(~uint32_t(w >> 32));
+      } else {
+        i = int(surv[r]);
+        v = sc[i];
+      }
+      if (!(v > ninf)) continue;
+      const float gk = v + gumbel(draw_uniform(p.seed, step, i));
+      if (better(gk, i, bv, bi)) {
+        bv = gk;
+        bi = i;
+      }
+    }
+  } else {
+    // 4d. nucleus over survivors sorted by (value desc, index asc)
+    bool in_lds = true;
+    if (!sorted && n_s <= kRankSort) {
+      if (!in_stage) {
+        for (int r = tid; r < n_s; r += kT) {
+          const uint32_t i = surv[r];
+          sh.stage[r] = row_word(order_key(sc[i]), i);
+        }
+        __syncthreads();
+      }
+      rank_sort(sh.stage, n_s, key, idx);
+    } else if (!sorted) {
+      int P = 1;
+      while (P < n_s) P <<= 1;
+      in_lds = P <= kSortLds;
+      if (!in_lds) {
+        key = p.scratch_u + n;
+        idx = p.scratch_u + n + P;
+      }
+      for (int r = tid; r < P; r += kT) {
+        if (r >= n_s) {
+          key[r] = 0xffffffffu;
+          idx[r] = 0x7fffffffu;
+        } else if (in_stage) {
+          const uint64_t w = sh.stage[r];
+          key[r] = uint32_t(w >> 32);
+          idx[r] = uint32_t(w);
+        } else {
+          const uint32_t i = surv[r];
+          key[r] = ~order_key(sc[i]);
+          idx[r] = i;
+        }
+      }
+      __syncthreads();
+      bitonic(key, idx, P);
+    }
+    float *prob = in_lds ? sh.prob : reinterpret_cast<float *>(surv);
+    uint8_t *keep = in_lds ? sh.keep : nullptr;
+    const float m = key_value(~key[0]);
+    // the draw's Gumbel keys are formed here too, beside the exponentials,
+    // while one wave runs the sequential sums below (in sh.slice, when the
+    // survivors fit)
+    const bool keyed = n_s <= 2 * kList;
+    for (int r = tid; r < n_s; r += kT) {
+      const float v = key_value(~key[r]);
+      prob[r] = m == ninf ? 0.f : portable_exp(v - m);
+      if (keyed)
+        sh.slice[r] = __builtin_bit_cast(uint32_t, v + gumbel(draw_uniform(p.seed, step, int(idx[r]))));
+    }
+    __syncthreads();
+    // sequential sums in sorted order, on one wave: 64 values at a time
+    // are loaded and divided in parallel and the running sums step through
+    // them lane by lane. Zeros after the last survivor leave both sums as
+    // they are.
+    if (tid < 64) {
+      const int lane = tid;
+      float total = 0.f;
+      for (int r0 = 0; r0 < n_s; r0 += 64) {
+        const float pv = r0 + lane < n_s ? prob[r0 + lane] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 64; ++j)
+          total += lane_value(pv, j);
+      }
+      const int minimum = cx.legacy ? 3 : 1;
+      float cum = 0.f;
+      for (int r0 = 0; r0 < n_s; r0 += 64) {
+        const int r = r0 + lane;
+        const float pv = r < n_s ? prob[r] : 0.f;
+        const float pr = cx.legacy ? rbf(pv / total) : pv / total;
+        float cum_r = 0.f;
+        if (cx.legacy) {  // uniform: the bf16 rounding stays out of the plain chain
+#pragma unroll
+          for (int j = 0; j < 64; ++j) {
+            cum = rbf(cum + lane_value(pr, j));
+            cum_r = lane == j ? cum : cum_r;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 64; ++j) {
+            cum = cum + lane_value(pr, j);
+            cum_r = lane == j ? cum : cum_r;
+          }
+        }
+        if (r < n_s) {
+          const float pre = cx.cast(cum_r - pr);
+          const bool removed = pre > p.top_p && r >= minimum;
+          if (keep)
+            keep[r] = !removed;
+          else
+            prob[r] = removed ? 0.f : 1.f;
+        }
+      }
+    }
+    __syncthreads();
+    for (int r = tid; r < n_s; r += kT) {
+      const bool kept = keep ? keep[r] != 0 : prob[r] != 0.f;
+      if (!kept) continue;
+      const int i = int(idx[r]);
+      const float v = key_value(~key[r]);
+      if (!(v > ninf)) continue;
+      const float gk = keyed ? __builtin_bit_cast(float, sh.slice[r])
+                             : v + gumbel(draw_uniform(p.seed, step, i));
+      if (better(gk, i, bv, bi)) {
+        bv = gk;
+        bi = i;
+      }
+    }
+  }
+  float rv;
+  int local;
+  block_argmax(bv, bi, sh, &rv, &local);
+  return local == 0x7fffffff ? 0 : local;
+}
+
+// The whole draw by one workgroup (kGreedy: with the temperature-0 path).
+template <bool kGreedy>
+__device__ __forceinline__ int sample_block(const SamplerParams &p, Shared &sh, int step) {
   const int tid = threadIdx.x;
   const int n = p.n;
-  if (p.state[1])
-    return;  // the end token was already drawn
-  const int step = p.state[0];
-  const bool greedy = p.temperature == 0.f;
+  const bool greedy = kGreedy && p.temperature == 0.f;
   const Ctx cx{p, p.legacy_off != 0, p.branches == 2 && p.cfg_scale != 1.0f, -__builtin_inff()};
   const float ninf = cx.ninf;
   const int end = p.phase == kPhaseAbc ? kEOD : p.phase == kPhaseSemantic ? 0 : -1;
@@ -329,56 +628,12 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
     for (int u = 0; u < kPre; ++u)
       pre[u] = reinterpret_cast<const u32x4 *>(p.logits)[min(tid + u * kT, max(n8 - 1, 0))];
   }
-
-  // Special rows: the end row while masked and the distinct local ids of the
-  // penalty window (sampling.cpp:51-75); everything else is a plain score.
-  const int nw = (n + 31) >> 5;
-  for (int i = tid; i < nw; i += kT)
-    sh.u.bits[i] = 0;
-  if (!greedy)
-    for (int i = tid; i < kBins; i += kT)
-      sh.hist[i] = 0;
-  if (tid == 0) {
-    sh.count = 0;
-    sh.n_surv = 0;
-    sh.end_penalised = 0;
-  }
-  const int hlen = p.hist_len < 0 ? step : p.hist_len;
-  const int wlen = p.alphas && p.penalty_window > 0 ? min(hlen, p.penalty_window) : 0;
-  if (tid < wlen)
-    sh.pen_loc[tid] = local_of(p.history[hlen - wlen + tid], p.phase, p.vocab);
-  __syncthreads();
-  int pen_count = 0;  // > 0: this thread owns a distinct penalised row
-  if (tid < wlen) {
-    const int loc = sh.pen_loc[tid];
-    bool first = loc >= 0 && loc < n;
-    for (int t = 0; t < wlen; ++t)
-      if (sh.pen_loc[t] == loc) {
-        ++pen_count;
-        if (t < tid) first = false;
-      }
-    if (first)
-      atomicOr(&sh.u.bits[loc >> 5], 1u << (loc & 31));
-    else
-      pen_count = 0;
-    if (pen_count > 0 && loc == end && end_masked)
-      sh.end_penalised = 1;
-  }
-  if (tid == 0 && end_masked)
-    atomicOr(&sh.u.bits[end >> 5], 1u << (end & 31));
-  __syncthreads();
-  // full score of a special row: mask, then penalty (a masked -inf stays -inf)
+  // > 0: this thread owns a distinct penalised row; everything else is a
+  // plain score
+  const int pen_count = mark_specials(p, sh, step, end, end_masked, 0, n, !greedy);
   auto special_score = [&](int loc, int count) {
-    float v = cx.one(loc);
-    if (loc == end && end_masked)
-      v = ninf;
-    if (count > 0) {
-      const float a = p.alphas[count];
-      v = v < 0.f ? cx.cast(v * a) : cx.cast(v / a);
-    }
-    return v;
+    return ::yuear::special_score(p, cx, loc, count, end, end_masked);
   };
-
   int local = 0;
   if (greedy) {  // sampling.cpp:247: argmax, lowest index on ties
     // Scan of this thread's logits; with kCheck the special rows (an LDS
@@ -514,10 +769,8 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
     // other two digits (11, 8 bits), and without room every pass reads the
     // scores instead.
     const int n4 = n >> 2;
-    uint32_t *key = sh.u.sort.key, *idx = sh.u.sort.idx;  // sorted survivors
-    bool in_list = false;  // survivors are in sh.stage (else in surv)
-    bool sorted = false;   // key/idx hold the n_s survivors in order
-    int n_s = 0;
+    bool in_list = false;  // the rows at or above the cut first digit are in sh.list
+    bool sorted = false;   // survivors sorted into the LDS key/idx arrays
     if (select) {
       int digit, krem, in_digit;
       find_cut(sh, k, &digit, &krem, &in_digit);
@@ -550,16 +803,7 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
             sh.list[slot] = row_word(key_i, uint32_t(i));
         }
         __syncthreads();
-      }
-      if (in_list && L <= kRankSort) {
-        rank_sort(sh.list, L, key, idx);
-        // survivors: the sorted prefix down to the k-th largest score, with
-        // every row tied with it
-        const uint32_t cut = key[k - 1];
-        for (int r = tid; r < L; r += kT)
-          if (key[r] <= cut)
-            atomicMax(&sh.n_surv, r + 1);
-        sorted = true;
+        sorted = select_in_list(sh, L, L, k, prefix, pmask, krem);
       } else {
         for (int pass = 1; pass < 3; ++pass) {
           const int shift = pass == 1 ? kShift1 : 0;
@@ -567,28 +811,20 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
           for (int i = tid; i < kBins; i += kT)
             sh.hist[i] = 0;
           __syncthreads();
-          if (in_list) {
-            for (int i = tid; i < L; i += kT) {
-              const uint32_t key_i = ~uint32_t(sh.list[i] >> 32);
-              if ((key_i & pmask) == prefix)
-                atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
-            }
-          } else {
-            for (int c = tid; c < n4; c += kT) {
-              const float4 f = reinterpret_cast<const float4 *>(sc)[c];
-              const float fv[4] = {f.x, f.y, f.z, f.w};
+          for (int c = tid; c < n4; c += kT) {
+            const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+            const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const uint32_t key_e = order_key(fv[e]);
-                if ((key_e & pmask) == prefix)
-                  atomicAdd(&sh.hist[(key_e >> shift) & dmask], 1u);
-              }
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t key_e = order_key(fv[e]);
+              if ((key_e & pmask) == prefix)
+                atomicAdd(&sh.hist[(key_e >> shift) & dmask], 1u);
             }
-            for (int i = 4 * n4 + tid; i < n; i += kT) {
-              const uint32_t key_i = order_key(sc[i]);
-              if ((key_i & pmask) == prefix)
-                atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
-            }
+          }
+          for (int i = 4 * n4 + tid; i < n; i += kT) {
+            const uint32_t key_i = order_key(sc[i]);
+            if ((key_i & pmask) == prefix)
+              atomicAdd(&sh.hist[(key_i >> shift) & dmask], 1u);
           }
           __syncthreads();
           int d, in_d;
@@ -596,29 +832,18 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
           prefix |= uint32_t(d) << shift;
           pmask |= dmask << shift;
         }
-        // 4c. survivors (key >= prefix, ties at the cut kept), compacted in
-        // any order: the nucleus sort and the draw's index tie-break restore
-        // determinism
-        if (in_list) {
-          for (int i = tid; i < L; i += kT) {
-            const uint64_t w = sh.list[i];
-            const int slot = wave_append(~uint32_t(w >> 32) >= prefix, &sh.n_surv);
-            if (slot >= 0)
-              sh.stage[slot] = w;
-          }
-        } else {
-          for (int c = tid; c < n4; c += kT) {
-            const float4 f = reinterpret_cast<const float4 *>(sc)[c];
-            const float fv[4] = {f.x, f.y, f.z, f.w};
+        // 4c. survivors (key >= prefix, ties at the cut kept), in any order
+        for (int c = tid; c < n4; c += kT) {
+          const float4 f = reinterpret_cast<const float4 *>(sc)[c];
+          const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (order_key(fv[e]) >= prefix)
-                surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(4 * c + e);
-          }
-          for (int i = 4 * n4 + tid; i < n; i += kT)
-            if (order_key(sc[i]) >= prefix)
-              surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(i);
+          for (int e = 0; e < 4; ++e)
+            if (order_key(fv[e]) >= prefix)
+              surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(4 * c + e);
         }
+        for (int i = 4 * n4 + tid; i < n; i += kT)
+          if (order_key(sc[i]) >= prefix)
+            surv[atomicAdd(&sh.n_surv, 1)] = uint32_t(i);
       }
     } else {  // every row survives
       for (int i = tid; i < n; i += kT)
@@ -627,143 +852,289 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
         sh.n_surv = n;
     }
     __syncthreads();
-    n_s = sh.n_surv;
+    local = draw_survivors(p, sh, cx, step, sh.n_surv, sorted, in_list);
+  }
 
+  return local;
+}
+
+// The chosen local row becomes the next input token of every branch, the
+// history entry and the step counter (sampling.cpp:249-260).
+__device__ void emit_token(const SamplerParams &p, int local, int step) {
+  if (threadIdx.x != 0)
+    return;
+  const int end = p.phase == kPhaseAbc ? kEOD : p.phase == kPhaseSemantic ? 0 : -1;
+  const int native = native_of(local, p.phase);
+  for (int b = 0; b < p.branches; ++b)
+    p.tokens_out[b] = native;
+  if (local == end)
+    p.state[1] = 1;
+  else if (step < p.max_tokens)
+    p.history[step] = native;
+  p.state[0] = step + 1;
+}
+
+// One workgroup per request (or per sequence with `independent`).
+__global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
+  __shared__ Shared sh;
+  SamplerParams p = p0;
+  if (p0.independent) {  // workgroup b: branch b on its own, as a 1-branch request
+    const int b = blockIdx.x;
+    p.logits += size_t(b) * p0.ls;
+    p.branches = 1;
+    p.state += 2 * b;
+    p.history += size_t(b) * p0.history_stride;
+    p.tokens_out += b;
+    p.scratch += size_t(b) * p0.scratch_stride;
+    p.scratch_u += size_t(b) * p0.scratch_u_stride;
+    p.seed += uint64_t(b);
+  }
+  if (p.state[1])
+    return;  // the end token was already drawn
+  const int step = p.state[0];
+  emit_token(p, sample_block<true>(p, sh, step), step);
+}
+
+// One request over gridDim.x workgroups, workgroup w on rows
+// [w * split_rows, (w + 1) * split_rows) (split_rows a multiple of 8, at
+// most 2 * kList, so one 8-row chunk per thread):
+//  - greedy: the workgroup's best (score, row) with the single-workgroup
+//    rules (special rows skipped, penalised rows rescored);
+//  - sampling: the scores' order keys in LDS, counted by first digit; the
+//    rows at or above the digit of the workgroup's own k-th largest (a
+//    superset of its share of the global top k, ties included) go to its
+//    region of a global array of row words (p.scratch_u), their count to
+//    p.scratch (as int).
+// Results go out with write-through stores; after they complete each
+// workgroup counts its arrival (device-scope counter p.sync[0]), and the
+// last one reads them back past the per-XCD L2 (agent-scope loads), finishes
+// the selection and the draw, emits the token and returns the counters to
+// zero. A list longer than kList sends the last workgroup through the
+// single-workgroup algorithm instead.
+__global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
+  __shared__ Shared sh;
+  if (p.state[1])
+    return;  // the end token was already drawn (the same for every workgroup)
+  const int step = p.state[0];
+  const int tid = threadIdx.x, n = p.n, G = gridDim.x;
+  const bool greedy = p.temperature == 0.f;
+  const Ctx cx{p, p.legacy_off != 0, p.branches == 2 && p.cfg_scale != 1.0f, -__builtin_inff()};
+  const float ninf = cx.ninf;
+  const int end = p.phase == kPhaseAbc ? kEOD : p.phase == kPhaseSemantic ? 0 : -1;
+  const bool end_masked = end >= 0 && end < n && step < p.min_tokens;  // sampling.cpp:47-50
+  const int lo = int(blockIdx.x) * p.split_rows, hi = min(n, lo + p.split_rows);
+  const int n8 = n >> 3;
+  const int c_lo = lo >> 3, c_hi = min(hi >> 3, n8);  // whole 8-row chunks of the slice
+  // this thread's chunk of logits (both branches) is loaded first, so its
+  // latency overlaps the special-row set-up
+  const int c = c_lo + int(tid);
+  const int cc = min(c, max(n8 - 1, 0));
+  const u32x4 la = reinterpret_cast<const u32x4 *>(p.logits)[cc];
+  const u32x4 lu = cx.cfg ? reinterpret_cast<const u32x4 *>(p.logits + p.ls)[cc] : la;
+  const int pen_count = mark_specials(p, sh, step, end, end_masked, lo, hi - lo, !greedy);
+  auto penalised_here = [&](int &loc) {
+    loc = pen_count > 0 ? sh.pen_loc[tid] : -1;
+    return loc >= lo && loc < hi;
+  };
+  uint64_t *cand = reinterpret_cast<uint64_t *>(p.scratch_u);  // [n] candidate row words
+  int32_t *counts = reinterpret_cast<int32_t *>(p.scratch);  // [G] candidates per workgroup
+  int32_t *sync = p.sync;
+
+  if (greedy) {  // sampling.cpp:247: argmax, lowest index on ties
     float bv = ninf;
     int bi = 0x7fffffff;
-    if (p.top_p >= 1.0f) {
-      // 4e. draw over the survivors (Gumbel-max)
-      for (int r = tid; r < n_s; r += kT) {
-        int i;
-        float v;
-        if (sorted) {
-          i = int(idx[r]);
-          v = key_value(~key[r]);
-        } else if (in_list) {
-          const uint64_t w = sh.stage[r];
-          i = int(uint32_t(w));
-          v = key_value(~uint32_t(w >> 32));
-        } else {
-          i = int(surv[r]);
-          v = sc[i];
-        }
-        if (!(v > ninf)) continue;
-        const float gk = v + gumbel(draw_uniform(p.seed, step, i));
-        if (better(gk, i, bv, bi)) {
-          bv = gk;
-          bi = i;
-        }
-      }
-    } else {
-      // 4d. nucleus over survivors sorted by (value desc, index asc)
-      bool in_lds = true;
-      if (!sorted && n_s <= kRankSort) {
-        if (!in_list) {
-          for (int r = tid; r < n_s; r += kT) {
-            const uint32_t i = surv[r];
-            sh.stage[r] = row_word(order_key(sc[i]), i);
-          }
-          __syncthreads();
-        }
-        rank_sort(sh.stage, n_s, key, idx);
-      } else if (!sorted) {
-        int P = 1;
-        while (P < n_s) P <<= 1;
-        in_lds = P <= kSortLds;
-        if (!in_lds) {
-          key = p.scratch_u + n;
-          idx = p.scratch_u + n + P;
-        }
-        for (int r = tid; r < P; r += kT) {
-          if (r >= n_s) {
-            key[r] = 0xffffffffu;
-            idx[r] = 0x7fffffffu;
-          } else if (in_list) {
-            const uint64_t w = sh.stage[r];
-            key[r] = uint32_t(w >> 32);
-            idx[r] = uint32_t(w);
-          } else {
-            const uint32_t i = surv[r];
-            key[r] = ~order_key(sc[i]);
-            idx[r] = i;
-          }
-        }
-        __syncthreads();
-        bitonic(key, idx, P);
-      }
-      float *prob = in_lds ? sh.prob : reinterpret_cast<float *>(surv);
-      uint8_t *keep = in_lds ? sh.keep : nullptr;
-      const float m = key_value(~key[0]);
-      for (int r = tid; r < n_s; r += kT)
-        prob[r] = m == ninf ? 0.f : portable_exp(key_value(~key[r]) - m);
-      __syncthreads();
-      // sequential sums in sorted order, on one wave: 64 values at a time
-      // are loaded and divided in parallel and the running sums step through
-      // them lane by lane. Zeros after the last survivor leave both sums as
-      // they are.
-      if (tid < 64) {
-        const int lane = tid;
-        float total = 0.f;
-        for (int r0 = 0; r0 < n_s; r0 += 64) {
-          const float pv = r0 + lane < n_s ? prob[r0 + lane] : 0.f;
+    if (c < c_hi) {
+      float v[8];
+      cx.merge(la, lu, v);
 #pragma unroll
-          for (int j = 0; j < 64; ++j)
-            total += lane_value(pv, j);
+      for (int e = 0; e < 8; ++e)
+        if (!special(sh, 8 * c + e - lo) && better(v[e], 8 * c + e, bv, bi)) {
+          bv = v[e];
+          bi = 8 * c + e;
         }
-        const int minimum = cx.legacy ? 3 : 1;
-        float cum = 0.f;
-        for (int r0 = 0; r0 < n_s; r0 += 64) {
-          const int r = r0 + lane;
-          const float pv = r < n_s ? prob[r] : 0.f;
-          const float pr = cx.legacy ? rbf(pv / total) : pv / total;
-          float cum_r = 0.f;
+    }
+    for (int i = max(lo, 8 * n8) + tid; i < hi; i += kT)
+      if (!special(sh, i - lo) && better(cx.one(i), i, bv, bi)) {
+        bv = cx.one(i);
+        bi = i;
+      }
+    int loc;
+    if (penalised_here(loc)) {
+      const float v = special_score(p, cx, loc, pen_count, end, end_masked);
+      if (better(v, loc, bv, bi)) {
+        bv = v;
+        bi = loc;
+      }
+    }
+    float rv;
+    int ri;
+    block_argmax(bv, bi, sh, &rv, &ri);
+    if (tid == 0) {
+      __hip_atomic_store(&p.scratch[blockIdx.x], rv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.scratch_u[blockIdx.x], uint32_t(ri), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    const int k = min(p.top_k, n);
+    // 4a. scores of the slice (sampling.cpp:44-81) as order keys, counted by
+    // their first digit
+    if (c < c_hi) {
+      float v[8];
+      cx.merge(la, lu, v);
 #pragma unroll
-          for (int j = 0; j < 64; ++j) {
-            cum = cx.cast(cum + lane_value(pr, j));
-            cum_r = lane == j ? cum : cum_r;
-          }
-          if (r < n_s) {
-            const float pre = cx.cast(cum_r - pr);
-            const bool removed = pre > p.top_p && r >= minimum;
-            if (keep)
-              keep[r] = !removed;
-            else
-              prob[r] = removed ? 0.f : 1.f;
-          }
-        }
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t key = order_key(cx.temp(v[e]));
+        sh.slice[8 * c + e - lo] = key;
+        atomicAdd(&sh.hist[key >> kShift0], 1u);
+      }
+    }
+    for (int i = max(lo, 8 * n8) + tid; i < hi; i += kT) {
+      const uint32_t key = order_key(cx.temp(cx.one(i)));
+      sh.slice[i - lo] = key;
+      atomicAdd(&sh.hist[key >> kShift0], 1u);
+    }
+    __syncthreads();
+    // special rows of the slice: the final score replaces the plain one
+    auto patch = [&](int loc, float s) {
+      const uint32_t key = order_key(s);
+      atomicSub(&sh.hist[sh.slice[loc - lo] >> kShift0], 1u);
+      atomicAdd(&sh.hist[key >> kShift0], 1u);
+      sh.slice[loc - lo] = key;
+    };
+    int loc;
+    if (penalised_here(loc))
+      patch(loc, cx.temp(special_score(p, cx, loc, pen_count, end, end_masked)));
+    if (tid == 0 && end_masked && !sh.end_penalised && end >= lo && end < hi)
+      patch(end, ninf);
+    __syncthreads();
+    // 4b, first part: the candidates of this slice, compacted in LDS and
+    // written to the workgroup's own region cand[lo, lo + count); the count
+    // goes out beside them (a count above kBins / 2 leaves the region empty:
+    // the total then exceeds kList and the last workgroup takes the
+    // single-workgroup path)
+    int digit, krem, in_digit;
+    const int kw = min(k, hi - lo);
+    find_cut(sh, kw, &digit, &krem, &in_digit);
+    const uint32_t prefix = uint32_t(digit) << kShift0;
+    const int count = kw - krem + in_digit;
+    if (count <= kBins / 2) {
+      for (int r = tid; r < hi - lo; r += kT) {
+        const uint32_t key = sh.slice[r];
+        const int slot = wave_append(key >= prefix, &sh.count);
+        if (slot >= 0 && slot < kBins / 2)
+          sh.stage[slot] = row_word(key, uint32_t(lo + r));
       }
       __syncthreads();
-      for (int r = tid; r < n_s; r += kT) {
-        const bool kept = keep ? keep[r] != 0 : prob[r] != 0.f;
-        if (!kept) continue;
-        const int i = int(idx[r]);
-        const float v = key_value(~key[r]);
-        if (!(v > ninf)) continue;
-        const float gk = v + gumbel(draw_uniform(p.seed, step, i));
-        if (better(gk, i, bv, bi)) {
-          bv = gk;
-          bi = i;
-        }
-      }
+      for (int j = tid; j < count; j += kT)
+        __hip_atomic_store(&cand[lo + j], sh.stage[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0)
+      __hip_atomic_store(&counts[blockIdx.x], count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // ---- arrival: every wave waits for its write-through stores to complete
+  // (a barrier alone does not wait for memory), then one count per
+  // workgroup; the last one to arrive finishes ----
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0)
+    sh.is_last = __hip_atomic_fetch_add(&sync[0], 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+  __syncthreads();
+  if (!sh.is_last)
+    return;
+
+  int local = 0;
+  if (greedy) {
+    float bv = ninf;
+    int bi = 0x7fffffff;
+    if (tid < G) {
+      bv = __hip_atomic_load(&p.scratch[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bi = int(__hip_atomic_load(&p.scratch_u[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
     float rv;
     block_argmax(bv, bi, sh, &rv, &local);
     if (local == 0x7fffffff) local = 0;
+  } else {
+    const int k = min(p.top_k, n);
+    // offsets of the workgroups' candidates in the gathered list (wave 0)
+    if (tid < 64) {
+      const int c = tid < G ? __hip_atomic_load(&counts[tid], __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0;
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (tid >= o) incl += t;
+      }
+      if (tid < kMaxGroups)  // first list slot of workgroup tid (past the end: unused)
+        sh.pen_loc[tid] = tid < G ? incl - c : 0x7fffffff;
+      if (tid == 63)
+        sh.bcast[3] = incl;
+    }
+    __syncthreads();
+    const int C = sh.bcast[3];
+    if (C <= kList) {
+      // 4b, second part: every candidate into LDS, its first digit counted
+      int first[kMaxGroups];
+#pragma unroll
+      for (int v = 0; v < kMaxGroups; ++v)
+        first[v] = sh.pen_loc[v];
+      for (int i = tid; i < C; i += kT) {
+        int w = 0;  // the workgroup whose candidates hold list slot i
+#pragma unroll
+        for (int v = 1; v < kMaxGroups; ++v)
+          w += first[v] <= i;
+        int base = 0;
+#pragma unroll
+        for (int v = 0; v < kMaxGroups; ++v)
+          base = v == w ? first[v] : base;
+        sh.list[i] = __hip_atomic_load(&cand[w * p.split_rows + (i - base)], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      }
+      for (int i = tid; i < kBins; i += kT)
+        sh.hist[i] = 0;
+      if (tid == 0) {
+        sh.count = 0;
+        sh.n_surv = 0;
+      }
+      __syncthreads();
+      for (int i = tid; i < C; i += kT)
+        atomicAdd(&sh.hist[~uint32_t(sh.list[i] >> 32) >> kShift0], 1u);
+      __syncthreads();
+      int digit, krem, in_digit;
+      find_cut(sh, k, &digit, &krem, &in_digit);
+      const uint32_t prefix = uint32_t(digit) << kShift0;
+      const bool sorted =
+          select_in_list(sh, C, k - krem + in_digit, k, prefix, ~0u << kShift0, krem);
+      __syncthreads();
+      local = draw_survivors(p, sh, cx, step, sh.n_surv, sorted, true);
+    } else {
+      __syncthreads();
+      local = sample_block<false>(p, sh, step);
+    }
   }
-
-  if (tid == 0) {  // sampling.cpp:249-260
-    const int native = native_of(local, p.phase);
-    for (int b = 0; b < p.branches; ++b)
-      p.tokens_out[b] = native;
-    if (local == end)
-      p.state[1] = 1;
-    else if (step < p.max_tokens)
-      p.history[step] = native;
-    p.state[0] = step + 1;
-  }
+  emit_token(p, local, step);
+  if (tid == 0)
+    __hip_atomic_store(&sync[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
+
+static int sampler_split_rows(const SamplerParams &p) {
+  // One 8-row chunk per thread in workgroups of about 8192 rows; greedy, or
+  // a shared draw whose top k leaves the candidate list (about k plus the
+  // cut digit's rows per workgroup) well inside LDS.
+  const int k = std::min(p.top_k, p.n);
+  if (p.independent || !p.sync || p.n <= 2 * kList ||
+      !(p.temperature == 0.f || (k < p.n && k <= kSplitMaxTopK)))
+    return 0;
+  const int groups = (p.n + 2 * kList - 1) / (2 * kList);
+  if (groups > kMaxGroups)
+    return 0;
+  return ((p.n + groups - 1) / groups + 7) / 8 * 8;
+}
 
 hipError_t launch_sampler(const SamplerParams &p, hipStream_t s) {
   if (p.n < 1 || p.n > 64 * kSortLds || p.ls < p.n || p.ls % 8 || p.branches < 1 ||
@@ -772,7 +1143,14 @@ hipError_t launch_sampler(const SamplerParams &p, hipStream_t s) {
       (p.independent && (p.history_stride < p.max_tokens || p.scratch_stride < p.n ||
                          p.scratch_u_stride < p.n)))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sampler_kernel, dim3(p.independent ? p.branches : 1), dim3(kT), 0, s, p);
+  const int rows = sampler_split_rows(p);
+  if (rows > 0) {
+    SamplerParams q = p;
+    q.split_rows = rows;
+    hipLaunchKernelGGL(sampler_split_kernel, dim3((p.n + rows - 1) / rows), dim3(kT), 0, s, q);
+  } else {
+    hipLaunchKernelGGL(sampler_kernel, dim3(p.independent ? p.branches : 1), dim3(kT), 0, s, p);
+  }
   return hipGetLastError();
 }
 
