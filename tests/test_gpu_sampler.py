@@ -143,6 +143,45 @@ def test_sampler_end_row_both_penalised_and_masked(engine_yue2, oracle, top_k, t
     session.close()
 
 
+EOD, ABC_END = 151643, 151848
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p,branches,cfg", [
+    (1.0, 30, 0.9, 1, 1.0),   # the ABC defaults
+    (0.8, 100, 1.0, 2, 1.5),  # CFG pair, top k only
+    (0.0, 1, 1.0, 1, 1.0),    # greedy
+])
+def test_sampler_abc_phase_tail_rows(engine_yue2, oracle, temperature, top_k, top_p, branches,
+                                     cfg):
+    # 151644 local rows: the last 8-row chunk is partial (rows 151640-151643)
+    # and its last row is the end row (ABC_END), masked before min_tokens and
+    # here also inside the penalty window
+    rng = np.random.default_rng(31 + top_k)
+    sampling = dict(temperature=temperature, top_p=top_p, top_k=top_k, repetition_penalty=1.3,
+                    penalty_window=50, min_tokens=100, max_tokens=9000)
+    session = engine_yue2.session(branches, 64, "abc")
+    n = session.vocab
+    assert n == EOD + 1
+    for trial in range(9):
+        x = rng.normal(size=(branches, n)) * 2
+        hist = [int(t) for t in rng.integers(n - 200, n - 1, size=60)]
+        if trial % 3 != 2:
+            hist[-1 - trial] = ABC_END            # the end row penalised too
+        x[:, [t for t in hist[-50:] if t < n - 1]] += 4
+        x[:, n - 1] += 9                           # the end row would lead
+        x[:, n - 4:n - 1] += 5 * (trial % 2)       # the other tail rows lead next
+        logits = bf(x)
+        session.write_logits(logits)
+        step = 40 if trial % 3 else 150            # masked, masked, unmasked
+        seed = int(rng.integers(0, 2**62))
+        got = session.sample(sampling, seed, step, history=hist, cfg_scale=cfg)
+        want = oracle_token(oracle, logits, sampling, seed, step, hist, "abc", cfg)
+        assert got == want, (trial, got, want)
+        if step < 100:
+            assert got != ABC_END
+    session.close()
+
+
 @pytest.mark.parametrize("branches,cfg", [(1, 1.0), (2, 1.5)])
 def test_greedy_with_penalty_and_end_mask(engine_yue2, oracle, branches, cfg):
     # the greedy path rescored only the penalised / masked rows: odd phase
