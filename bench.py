@@ -360,7 +360,8 @@ def main():
     session = engine.session(1, capacity)
     rng = np.random.default_rng(args.seed)
     if args.kernel_only:
-        session.prefill(0, rng.integers(0, c["vocab_size"], size=64).tolist())
+        # the decode line's prompt length, so the attention reads its KV length
+        session.prefill(0, rng.integers(0, c["vocab_size"], size=prefill).tolist())
         ms = session.time_kernel(args.kernel_only, args.kernel_launches)
         print(json.dumps({"kernel": args.kernel_only, "launches": args.kernel_launches,
                           "us": ms * 1e3}), flush=True)
