@@ -66,3 +66,31 @@ def test_phase_slices_match_oracle_and_full_rows(pair, oracle):
     for phase in ("abc", "semantic"):
         for g, full in zip(got[phase], got["full"]):
             np.testing.assert_array_equal(g, rows_of(full, phase))
+
+
+def test_generate_tokens_abc_phase_draws_match_oracle(pair, oracle):
+    """generate_tokens in the abc phase (151644 rows: the sampler spread over
+    workgroups, the end row in the partial last chunk) with the ABC sampling
+    defaults, a penalty window and min_tokens: every token equals the
+    oracle's distribution + draw on the GPU's own logits, replayed step by
+    step through a session (the same kernels)."""
+    engine, _ = pair
+    rng = np.random.default_rng(5)
+    prefix = [EOD] + rng.integers(0, EOD, size=12).tolist()
+    sampling = dict(temperature=0.7, top_p=0.9, top_k=30, repetition_penalty=1.005,
+                    penalty_window=100, min_tokens=6, max_tokens=24)
+    seed = 77
+    tokens, _, _ = engine.generate_tokens(prefix, sampling, seed, phase="abc")
+    assert 6 <= len(tokens) <= 24
+    assert ABC_END not in tokens[:6]
+    s = engine.session(1, len(prefix) + 32, "abc")
+    logits = s.prefill(0, prefix)
+    ref = oracle.sampling_struct(**sampling)
+    for step, token in enumerate(tokens):
+        scores = oracle.distribution(logits, ref, tokens[:step], step, "abc")
+        local = oracle.draw(scores, sampling["temperature"], seed, step)
+        assert oracle.lib().oracle_local_to_native(local, oracle.PHASES["abc"]) == token, step
+        if token == ABC_END:
+            break
+        logits = s.step(token)[0]
+    s.close()
