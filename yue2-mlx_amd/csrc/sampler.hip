@@ -931,7 +931,13 @@ __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
   const int cc = min(c, max(n8 - 1, 0));
   const u32x4 la = reinterpret_cast<const u32x4 *>(p.logits)[cc];
   const u32x4 lu = cx.cfg ? reinterpret_cast<const u32x4 *>(p.logits + p.ls)[cc] : la;
-  const int pen_count = mark_specials(p, sh, step, end, end_masked, lo, hi - lo, !greedy);
+  // greedy with no special row (no penalty window, end row not masked)
+  // needs no set-up at all
+  const int hlen = p.hist_len < 0 ? step : p.hist_len;
+  const bool specials = end_masked || (p.alphas && p.penalty_window > 0 && hlen > 0);
+  const int pen_count = greedy && !specials
+                            ? 0
+                            : mark_specials(p, sh, step, end, end_masked, lo, hi - lo, !greedy);
   auto penalised_here = [&](int &loc) {
     loc = pen_count > 0 ? sh.pen_loc[tid] : -1;
     return loc >= lo && loc < hi;
@@ -948,13 +954,13 @@ __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
       cx.merge(la, lu, v);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (!special(sh, 8 * c + e - lo) && better(v[e], 8 * c + e, bv, bi)) {
+        if (!(specials && special(sh, 8 * c + e - lo)) && better(v[e], 8 * c + e, bv, bi)) {
           bv = v[e];
           bi = 8 * c + e;
         }
     }
     for (int i = max(lo, 8 * n8) + tid; i < hi; i += kT)
-      if (!special(sh, i - lo) && better(cx.one(i), i, bv, bi)) {
+      if (!(specials && special(sh, i - lo)) && better(cx.one(i), i, bv, bi)) {
         bv = cx.one(i);
         bi = i;
       }
@@ -1045,16 +1051,26 @@ __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
     return;
 
   int local = 0;
-  if (greedy) {
-    float bv = ninf;
-    int bi = 0x7fffffff;
-    if (tid < G) {
-      bv = __hip_atomic_load(&p.scratch[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bi = int(__hip_atomic_load(&p.scratch_u[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  if (greedy) {  // the slices' bests (at most kMaxGroups) on wave 0
+    if (tid < 64) {
+      float bv = ninf;
+      int bi = 0x7fffffff;
+      if (tid < G) {
+        bv = __hip_atomic_load(&p.scratch[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bi = int(__hip_atomic_load(&p.scratch_u[tid], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT));
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o, 64);
+        const int i2 = __shfl_xor(bi, o, 64);
+        if (better(v2, i2, bv, bi)) {
+          bv = v2;
+          bi = i2;
+        }
+      }
+      local = bi == 0x7fffffff ? 0 : bi;
     }
-    float rv;
-    block_argmax(bv, bi, sh, &rv, &local);
-    if (local == 0x7fffffff) local = 0;
   } else {
     const int k = min(p.top_k, n);
     // offsets of the workgroups' candidates in the gathered list (wave 0)
