@@ -898,8 +898,8 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
 // One request over gridDim.x workgroups, workgroup w on rows
 // [w * split_rows, (w + 1) * split_rows) (split_rows a multiple of 8, at
 // most 2 * kList, so one 8-row chunk per thread):
-//  - greedy: the workgroup's best (score, row) with the single-workgroup
-//    rules (special rows skipped, penalised rows rescored);
+//  - greedy: each wave's best (score, row) with the single-workgroup rules
+//    (special rows skipped, penalised rows rescored);
 //  - sampling: the scores' order keys in LDS, counted by first digit; the
 //    rows at or above the digit of the workgroup's own k-th largest (a
 //    superset of its share of the global top k, ties included) go to its
@@ -972,12 +972,20 @@ __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
         bi = loc;
       }
     }
-    float rv;
-    int ri;
-    block_argmax(bv, bi, sh, &rv, &ri);
-    if (tid == 0) {
-      __hip_atomic_store(&p.scratch[blockIdx.x], rv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.scratch_u[blockIdx.x], uint32_t(ri), __ATOMIC_RELAXED,
+    // each wave's best goes out on its own (no workgroup barrier)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v2 = __shfl_xor(bv, o, 64);
+      const int i2 = __shfl_xor(bi, o, 64);
+      if (better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
+    }
+    if ((tid & 63) == 0) {
+      const int slot = int(blockIdx.x) * kWaves + (tid >> 6);
+      __hip_atomic_store(&p.scratch[slot], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.scratch_u[slot], uint32_t(bi), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
   } else {
@@ -1051,15 +1059,27 @@ __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
     return;
 
   int local = 0;
-  if (greedy) {  // the slices' bests (at most kMaxGroups) on wave 0
+  if (greedy) {  // the waves' bests (at most kMaxGroups * kWaves) on wave 0
     if (tid < 64) {
+      constexpr int kPer = kMaxGroups * kWaves / 64;
+      const int total = G * kWaves;
+      float vs[kPer];
+      int is[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {  // one round of loads
+        const int e = min(int(tid) + 64 * j, total - 1);
+        vs[j] = __hip_atomic_load(&p.scratch[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is[j] = int(__hip_atomic_load(&p.scratch_u[e], __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT));
+      }
       float bv = ninf;
       int bi = 0x7fffffff;
-      if (tid < G) {
-        bv = __hip_atomic_load(&p.scratch[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bi = int(__hip_atomic_load(&p.scratch_u[tid], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT));
-      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j)
+        if (int(tid) + 64 * j < total && better(vs[j], is[j], bv, bi)) {
+          bv = vs[j];
+          bi = is[j];
+        }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) {
         const float v2 = __shfl_xor(bv, o, 64);
