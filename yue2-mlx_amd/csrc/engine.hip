@@ -272,7 +272,7 @@ struct yuear_session {
   float *scratch = nullptr, *alphas = nullptr;
   uint32_t *scratch_u = nullptr;
   int32_t *sstate = nullptr, *history = nullptr;
-  int32_t *sampler_sync = nullptr;  // split sampler counters, zero between launches
+  int32_t *sampler_sync = nullptr;  // split sampler arrival counter, zero between launches
   int history_cap = 0;       // history entries per branch set
   int scratch_u_stride = 0;
   // prefill scratch
@@ -644,8 +644,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.scratch = S.alloc<float>(size_t(S.phase.size) * sets);
   S.scratch_u = S.alloc<uint32_t>(size_t(S.scratch_u_stride) * sets);
   S.alphas = S.alloc<float>(128);
-  S.sampler_sync = S.alloc<int32_t>(2);
-  HIPC(hipMemsetAsync(S.sampler_sync, 0, 2 * sizeof(int32_t), S.stream));
+  S.sampler_sync = S.alloc<int32_t>(1);
+  HIPC(hipMemsetAsync(S.sampler_sync, 0, sizeof(int32_t), S.stream));
   S.sstate = S.alloc<int32_t>(2 * sets);
   S.history_cap = kContext;
   S.history = S.alloc<int32_t>(size_t(S.history_cap) * sets);

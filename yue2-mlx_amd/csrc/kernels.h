@@ -161,9 +161,9 @@ struct SamplerParams {
   // all branches (a request, or a CFG pair).
   int independent = 0;
   int history_stride = 0, scratch_stride = 0, scratch_u_stride = 0;
-  // [2] arrival and candidate counters, zero between launches: with them a
-  // shared draw (greedy, or top k up to 128) over more than 8192 rows is
-  // spread over one workgroup per ~8192 rows; null keeps one workgroup.
+  // [1] arrival counter, zero between launches: with it a shared draw
+  // (greedy, or top k up to 128) over more than 8192 rows is spread over one
+  // workgroup per ~8192 rows; null keeps one workgroup.
   int32_t *sync = nullptr;
   int split_rows = 0;  // set by launch_sampler
 };

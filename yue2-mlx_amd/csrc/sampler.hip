@@ -1,12 +1,17 @@
-// Device sampler: CFG merge + distribution() + draw, one workgroup.
+// Device sampler: CFG merge + distribution() + draw.
 //
 // Reference: native/src/sampling.cpp:38-134 (distribution, guided_logits,
 // RequestRNG) and sampling.cpp:242-260 (loop body). One launch produces the
 // next token entirely on the GPU, so the decode loop never waits on the host.
+// Two forms with the same arithmetic: sampler_split_kernel (a shared draw
+// over more than 8192 rows, greedy or top k up to 128: one workgroup per
+// ~8192 rows, the last to arrive finishing) and sampler_kernel (one
+// workgroup per request, or per sequence for batched sequences).
 //
 //  1. scores[i] = f32(logit) (bf16 when legacy_off), CFG-merged with the
 //     reference's three bf16 rounding points, end row masked before
-//     min_tokens; scores live in a global fp32 scratch (L2 resident).
+//     min_tokens (one workgroup: in a global fp32 scratch; split: as order
+//     keys in each workgroup's LDS).
 //  2. windowed repetition penalty on the distinct local ids of the last
 //     `penalty_window` emitted tokens, alpha = pow(p, count) from a host-built
 //     table (the lookup form of vendor fast.py:123-136).
@@ -341,8 +346,9 @@ __device__ __forceinline__ bool special(const Shared &sh, int i) {
 // first occurrence of a penalised row in the window (sh.pen_loc[tid]), the
 // row's count in the window, else 0. Also clears the histogram (when asked),
 // the list counters and end_penalised.
-__device__ __forceinline__ int mark_specials(const SamplerParams &p, Shared &sh, int step, int end,
-                             bool end_masked, int lo, int span, bool clear_hist) {
+__device__ __forceinline__ int mark_specials(const SamplerParams &p, Shared &sh, int step,
+                                             int end, bool end_masked, int lo, int span,
+                                             bool clear_hist) {
   const int tid = threadIdx.x;
   for (int i = tid; i < (span + 31) >> 5; i += kT)
     sh.u.bits[i] = 0;
@@ -404,8 +410,8 @@ __device__ __forceinline__ float special_score(const SamplerParams &p, const Ctx
 // survivors in key/idx. More rows go through the other two digits and the
 // survivors are left unsorted in sh.stage: returns false. sh.n_surv holds the
 // count after a barrier. sh.count must be 0.
-__device__ __forceinline__ bool select_in_list(Shared &sh, int L, int top, int k, uint32_t prefix,
-                               uint32_t pmask, int krem) {
+__device__ __forceinline__ bool select_in_list(Shared &sh, int L, int top, int k,
+                                               uint32_t prefix, uint32_t pmask, int krem) {
   const int tid = threadIdx.x;
   uint32_t *key = sh.u.sort.key, *idx = sh.u.sort.idx;
   if (top <= kRankSort) {
@@ -458,8 +464,8 @@ __device__ __forceinline__ bool select_in_list(Shared &sh, int L, int top, int k
 // 4d/4e. The draw among the n_s survivors: sorted in the LDS key/idx
 // arrays (sorted), unsorted in sh.stage (in_stage), or unsorted in
 // surv = p.scratch_u with their scores in p.scratch.
-__device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh, const Ctx &cx, int step,
-                              int n_s, bool sorted, bool in_stage) {
+__device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh, const Ctx &cx,
+                                              int step, int n_s, bool sorted, bool in_stage) {
   const int tid = threadIdx.x, n = p.n;
   const float ninf = cx.ninf;
   const float *sc = p.scratch;
@@ -538,7 +544,8 @@ __device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh
       const float v = key_value(~key[r]);
       prob[r] = m == ninf ? 0.f : portable_exp(v - m);
       if (keyed)
-        sh.slice[r] = __builtin_bit_cast(uint32_t, v + gumbel(draw_uniform(p.seed, step, int(idx[r]))));
+        sh.slice[r] =
+            __builtin_bit_cast(uint32_t, v + gumbel(draw_uniform(p.seed, step, int(idx[r]))));
     }
     __syncthreads();
     // sequential sums in sorted order, on one wave: 64 values at a time
@@ -908,7 +915,7 @@ __global__ __launch_bounds__(kT) void sampler_kernel(SamplerParams p0) {
 // Results go out with write-through stores; after they complete each
 // workgroup counts its arrival (device-scope counter p.sync[0]), and the
 // last one reads them back past the per-XCD L2 (agent-scope loads), finishes
-// the selection and the draw, emits the token and returns the counters to
+// the selection and the draw, emits the token and returns the counter to
 // zero. A list longer than kList sends the last workgroup through the
 // single-workgroup algorithm instead.
 __global__ __launch_bounds__(kT) void sampler_split_kernel(SamplerParams p) {
