@@ -623,7 +623,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.act = S.alloc<uint16_t>(size_t(branches) * c.F);
   S.logits = S.alloc<uint16_t>(size_t(branches) * S.phase.stride());
   // split-K: one 128-key pass per workgroup at the session's capacity, at
-  // most ~512 workgroups (attn_decode_splits); YUEAR_ATTN_SPLITS overrides.
+  // most one workgroup per CU for one sequence and ~512 workgroups for more
+  // branches (attn_decode_splits); YUEAR_ATTN_SPLITS overrides.
   {
     int splits = attn_decode_splits(branches, c.Hkv, S.kv_stride);
     if (const char *env = std::getenv("YUEAR_ATTN_SPLITS"))
