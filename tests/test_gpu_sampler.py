@@ -50,6 +50,10 @@ def logits_for(rng, kind, branches, n):
         x = rng.normal(size=(branches, n)) * 2.5
     elif kind == "ties":  # heavy ties at the top-k / nucleus cut
         x = np.round(rng.normal(size=(branches, n)) * 2) / 2
+    elif kind == "equal":  # every row tied: the candidate lists overflow LDS
+        x = np.full((branches, n), 1.25)
+    elif kind == "integers":  # ~300 rows tied at the 100th largest (4.0)
+        x = np.round(rng.normal(size=(branches, n)) * 1.3)
     elif kind == "peaked":
         x = rng.normal(size=(branches, n))
         x[:, rng.integers(0, n, 3)] += 12
@@ -68,10 +72,15 @@ CASES = [
     ("topp-flat", dict(temperature=1.0, top_k=5000, top_p=0.5), 1, 1.0, "full", "flat"),
     ("all-vocab", dict(temperature=1.3, top_k=100000, top_p=1.0), 1, 1.0, "full", "normal"),
     ("peaked", dict(temperature=1.0, top_k=100, top_p=0.95), 1, 1.0, "full", "peaked"),
-    # 257-512 survivors: the one-wave register sort at its largest size
+    # 257-512 survivors: the network sort in LDS
     ("topk-400", dict(temperature=1.0, top_k=400, top_p=0.9), 1, 1.0, "full", "normal"),
     # 1025-4096 survivors: the LDS sort of the rows gathered after the first digit
     ("topk-2000-cfg", dict(temperature=0.8, top_k=2000, top_p=0.8), 2, 1.5, "full", "normal"),
+    # top k in the split form's range: every row tied (the last workgroup
+    # falls back to the one-workgroup algorithm over all rows), and ~300
+    # rows at or above the cut (the merge's digit passes and network sort)
+    ("split-all-equal", dict(temperature=1.0, top_k=50, top_p=0.9), 1, 1.0, "full", "equal"),
+    ("split-ties-k100", dict(temperature=1.0, top_k=100, top_p=0.97), 1, 1.0, "full", "integers"),
 ]
 
 
