@@ -584,14 +584,40 @@ __device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh
         if (r < n_s) {
           const float pre = cx.cast(cum_r - pr);
           const bool removed = pre > p.top_p && r >= minimum;
-          if (keep)
+          if (keyed) {  // the draw on this wave: the best key of the kept rows
+            const float v = key_value(~key[r]);
+            const int i = int(idx[r]);
+            const float gk = __builtin_bit_cast(float, sh.slice[r]);
+            if (!removed && v > ninf && better(gk, i, bv, bi)) {
+              bv = gk;
+              bi = i;
+            }
+          } else if (keep) {
             keep[r] = !removed;
-          else
+          } else {
             prob[r] = removed ? 0.f : 1.f;
+          }
         }
+      }
+      if (keyed) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float v2 = __shfl_xor(bv, o, 64);
+          const int i2 = __shfl_xor(bi, o, 64);
+          if (better(v2, i2, bv, bi)) {
+            bv = v2;
+            bi = i2;
+          }
+        }
+        if (lane == 0)
+          sh.bcast[3] = bi;
       }
     }
     __syncthreads();
+    if (keyed) {
+      const int b = sh.bcast[3];
+      return b == 0x7fffffff ? 0 : b;
+    }
     for (int r = tid; r < n_s; r += kT) {
       const bool kept = keep ? keep[r] != 0 : prob[r] != 0.f;
       if (!kept) continue;
