@@ -536,9 +536,9 @@ __device__ __forceinline__ int draw_survivors(const SamplerParams &p, Shared &sh
     float *prob = in_lds ? sh.prob : reinterpret_cast<float *>(surv);
     uint8_t *keep = in_lds ? sh.keep : nullptr;
     const float m = key_value(~key[0]);
-    // the draw's Gumbel keys are formed here too, beside the exponentials,
-    // while one wave runs the sequential sums below (in sh.slice, when the
-    // survivors fit)
+    // the draw's Gumbel keys are formed here too, beside the exponentials
+    // (in sh.slice, when the survivors fit); the wave that runs the
+    // sequential sums below then takes the best kept key as it goes
     const bool keyed = n_s <= 2 * kList;
     for (int r = tid; r < n_s; r += kT) {
       const float v = key_value(~key[r]);
