@@ -231,6 +231,72 @@ def test_sampler_legacy_off_bf16_mode(engine_yue2, oracle):
     session.close()
 
 
+@pytest.fixture(scope="module")
+def engine_4096(yuear_lib):
+    return head_engine(yuear_lib, 4096)
+
+
+# (engine, phase, top_k, temperature): the split form serves more than 8192
+# rows at top k <= 128 and greedy; the one-workgroup form the rest.
+LEGACY_OFF_FORMS = {
+    "split-sampled": ("yue2", "semantic", 30, 1.0),
+    "one-wg-sampled": ("yue2", "semantic", 200, 1.0),
+    "split-greedy": ("yue2", "semantic", 1, 0.0),
+    "one-wg-greedy": ("4096", "full", 1, 0.0),
+}
+
+
+def _local(phase, native):
+    return native - MUSIC_END if phase == "semantic" else native
+
+
+@pytest.mark.parametrize("penalty", [1.005, 1.2])
+@pytest.mark.parametrize("form", sorted(LEGACY_OFF_FORMS))
+def test_sampler_legacy_off_penalised_rows_lead(engine_yue2, engine_4096, oracle, form, penalty):
+    # legacy-off (bf16) scores with the penalised history rows in the top k:
+    # alpha = pow(p, count) is cast to bf16 before it scales a score
+    # (sampling.cpp:67-70); with p = 1.005 that is 1.0078125, not 1.005
+    which, phase, top_k, temperature = LEGACY_OFF_FORMS[form]
+    engine = engine_yue2 if which == "yue2" else engine_4096
+    rng = np.random.default_rng(int(penalty * 1000) + top_k)
+    sampling = dict(temperature=temperature, top_p=0.95, top_k=top_k,
+                    repetition_penalty=penalty, penalty_window=50, min_tokens=0, max_tokens=9000)
+    session = engine.session(1, 64, phase)
+    n = session.vocab
+    base = CODEC_OFFSET if phase == "semantic" else 100
+    for trial in range(12):
+        x = rng.normal(size=(1, n)) * 2
+        hist = [base + int(t) for t in rng.integers(0, 40, size=int(rng.integers(20, 60)))]
+        x[0, [_local(phase, h) for h in hist[-50:]]] += 3  # penalised rows lead
+        logits = bf(x)
+        session.write_logits(logits)
+        seed = int(rng.integers(0, 2**62))
+        got = session.sample(sampling, seed, len(hist), history=hist, legacy_off=True)
+        want = oracle_token(oracle, logits, sampling, seed, len(hist), hist, phase, legacy=True)
+        assert got == want, (form, trial, got, want)
+    if penalty == 1.005:
+        # a penalised row at 7.0 against an unpenalised row at 6.9375 with a
+        # lower index: bf16(7 / bf16(1.005)) = 6.9375 ties it (the lower
+        # index wins, or the draw splits them evenly), while 7 / 1.005 in
+        # fp32 would round to 6.96875 and always win
+        u, pen = base + 4, base + 8
+        x = rng.normal(size=(1, n)) * 0.5
+        x[0, _local(phase, u)] = 6.9375
+        x[0, _local(phase, pen)] = 7.0
+        logits = bf(x)
+        session.write_logits(logits)
+        cold = dict(sampling, temperature=0.001 if temperature else 0.0)
+        picks = set()
+        for trial in range(12):
+            seed = int(rng.integers(0, 2**62))
+            got = session.sample(cold, seed, 1, history=[pen], legacy_off=True)
+            want = oracle_token(oracle, logits, cold, seed, 1, [pen], phase, legacy=True)
+            assert got == want, (form, "near tie", trial, got, want)
+            picks.add(want)
+        assert u in picks  # the case separates bf16 alpha from fp32 alpha
+    session.close()
+
+
 def test_sampler_known_answers_on_device(engine_yue2):
     # test_sampling.py:37-49 restated through the device sampler: only the
     # surviving rows can ever be drawn.

@@ -395,7 +395,8 @@ __device__ __forceinline__ float special_score(const SamplerParams &p, const Ctx
   if (loc == end && end_masked)
     v = cx.ninf;
   if (count > 0) {
-    const float a = p.alphas[count];
+    // alpha in the scores' dtype (sampling.cpp:67-70): bf16 in legacy-off mode
+    const float a = cx.cast(p.alphas[count]);
     v = v < 0.f ? cx.cast(v * a) : cx.cast(v / a);
   }
   return v;
