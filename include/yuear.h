@@ -88,6 +88,10 @@ typedef struct yuear_session yuear_session;
  * Runs synchronously on the calling thread; must not re-enter. */
 typedef void (*yuear_token_callback)(void *user_data, const char *phase, int32_t token);
 
+/* Cancellation poll (types.hpp:26 Cancelled): nonzero cancels the call.
+ * Runs synchronously on the calling thread, like the token callback. */
+typedef int32_t (*yuear_cancel_poll)(void *user_data);
+
 /* Borrowed build identity (lyra.h:29). */
 const char *yuear_build_identifier(void);
 void yuear_string_free(char *s); /* lyra.h:54 */
@@ -135,13 +139,22 @@ void yuear_random_tensor(uint64_t seed, int32_t tensor_id, float mean, float std
  * tokens_out receives up to sampling->max_tokens native ids; *n_out the
  * count, *truncated 1 when no end token was drawn; *timing_json the timing
  * keys of sampling.cpp:274-284. Draws use the shared Philox uniforms
- * u(seed, step, index). */
+ * u(seed, step, index).
+ * `cancelled` (may be NULL) and yuear_engine_cancel are checked where the
+ * reference polls its Cancelled predicate, with its messages (status 130,
+ * InterruptedError): after validation and at the start of each branch's
+ * prefill, "Cancelled before prefill" (sampling.cpp:156, 206); between
+ * prefill chunks, "Cancelled during prefill" (sampling.cpp:164); before each
+ * token is emitted, "Cancelled during <phase>" (sampling.cpp:243). A decode
+ * step runs as one graph, so the reference's per-layer poll inside a forward
+ * (ar.cpp:261-262) becomes the next per-token poll. Both callbacks receive
+ * `user_data`. */
 yuear_status yuear_generate_tokens(
     yuear_engine *engine, const int32_t *prefix, int32_t n_prefix,
     const yuear_sampling *sampling, uint64_t seed, const char *phase,
     const int32_t *negative, int32_t n_negative, double cfg_scale,
-    int32_t legacy_off, yuear_token_callback on_token, void *user_data,
-    int32_t *tokens_out, int32_t *n_out, int32_t *truncated,
+    int32_t legacy_off, yuear_cancel_poll cancelled, yuear_token_callback on_token,
+    void *user_data, int32_t *tokens_out, int32_t *n_out, int32_t *truncated,
     char **timing_json, char **error_json);
 
 /* ---- decode-step session (GraphAR, cuda_graph.py:43-240; KVCache,

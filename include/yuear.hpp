@@ -170,11 +170,23 @@ inline TokenGeneration generate_tokens(Engine &engine, const std::vector<int> &p
     try {
       if (*c->cb)
         (*c->cb)(ph, int(token));
-      if (*c->cancel && (*c->cancel)())
-        c->engine->cancel();  // polled once per token
     } catch (...) {
       c->thrown = std::current_exception();
       c->engine->cancel();
+    }
+  };
+  // polled by the library where the reference calls cancelled_at
+  // (sampling.cpp:156, 164, 206, 243); a throwing predicate cancels the call
+  // and its exception reaches the caller
+  auto poll = [](void *user) -> int32_t {
+    auto *c = static_cast<Ctx *>(user);
+    if (c->thrown)
+      return 1;
+    try {
+      return *c->cancel && (*c->cancel)() ? 1 : 0;
+    } catch (...) {
+      c->thrown = std::current_exception();
+      return 1;
     }
   };
   const std::vector<int32_t> pre(prefix.begin(), prefix.end());
@@ -185,7 +197,7 @@ inline TokenGeneration generate_tokens(Engine &engine, const std::vector<int> &p
   const std::string ph(phase);
   const yuear_status st = yuear_generate_tokens(
       engine.get(), pre.data(), int32_t(pre.size()), &ys, seed, ph.c_str(), neg.data(),
-      int32_t(neg.size()), cfg_scale, legacy_off ? 1 : 0, trampoline, &ctx, out.data(), &n,
+      int32_t(neg.size()), cfg_scale, legacy_off ? 1 : 0, poll, trampoline, &ctx, out.data(), &n,
       &truncated, &timing, &error);
   if (ctx.thrown) {
     yuear_string_free(timing);

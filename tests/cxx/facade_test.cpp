@@ -62,14 +62,31 @@ int main() {
     line("invalid", "\"error\":\"" + e.type + "\"");
   }
 
-  int calls = 0;
-  try {
-    yuear::generate_tokens(engine, prefix, sampled, 5, "full", {}, 1.0, false,
-                           [&] { return calls >= 3; },
-                           [&](std::string_view, int) { ++calls; });
-    line("cancelled", "\"error\":null");
-  } catch (const yuear::Error &e) {
-    line("cancelled", "\"error\":\"" + e.type + "\",\"calls\":" + std::to_string(calls));
+  // Cancellation where the reference polls (sampling.cpp:156, 164, 206,
+  // 243): `cancel_after` polls answer false, the rest true. With a CFG pair
+  // the polls come: after validation, before branch 0's prefill, its chunk,
+  // before branch 1's prefill, its chunk, then before each token.
+  struct Cancel {
+    const char *name;
+    int cancel_after, stop_after_calls;
+  };
+  for (const Cancel &k : {Cancel{"cancel_before", 0, -1}, Cancel{"cancel_branch1", 3, -1},
+                          Cancel{"cancel_prefill", 4, -1}, Cancel{"cancelled", -1, 3}}) {
+    int calls = 0, polls = 0;
+    try {
+      yuear::generate_tokens(
+          engine, prefix, sampled, 5, "full", {9, 8, 7}, 1.5, false,
+          [&] {
+            ++polls;
+            return k.cancel_after >= 0 ? polls > k.cancel_after : calls >= k.stop_after_calls;
+          },
+          [&](std::string_view, int) { ++calls; });
+      line(k.name, "\"error\":null");
+    } catch (const yuear::Error &e) {
+      line(k.name, "\"error\":\"" + e.type + "\",\"message\":\"" + e.what() +
+                       "\",\"calls\":" + std::to_string(calls) +
+                       ",\"polls\":" + std::to_string(polls));
+    }
   }
 
   try {

@@ -219,6 +219,46 @@ def test_throwing_callback_cancels(tiny):
     assert len(tokens) == 30
 
 
+def test_cancel_points_and_messages(yuear_lib):
+    # the reference polls its Cancelled predicate after validation and at
+    # the start of each prefill ("Cancelled before prefill", sampling.cpp:156,
+    # 206), before every 1024-token prefill chunk ("Cancelled during prefill",
+    # :164) and before every step ("Cancelled during <phase>", :243); the
+    # library polls at the same points (its chunks hold up to 4096 tokens, so
+    # a 9000-token prefix is three chunks) and reports nothing after a cancel
+    cfg = dict(TINY, max_position_embeddings=16384)
+    engine = yuear_lib.Engine(cfg, seed=3)
+    prefix = [int(t) for t in np.random.default_rng(0).integers(0, cfg["vocab_size"], 9000)]
+    sampling = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
+                    penalty_window=50, min_tokens=0, max_tokens=16)
+    for answer_false, message in [(0, "Cancelled before prefill"),
+                                  (1, "Cancelled before prefill"),
+                                  (2, "Cancelled during prefill"),
+                                  (4, "Cancelled during prefill"),
+                                  (5, "Cancelled during full"),
+                                  (8, "Cancelled during full")]:
+        polls, calls, at_cancel = [], [], []
+
+        def cancelled():
+            polls.append(1)
+            if len(polls) > answer_false and not at_cancel:
+                at_cancel.append(len(calls))
+            return len(polls) > answer_false
+
+        with pytest.raises(InterruptedError, match=message):
+            engine.generate_tokens(prefix, sampling, 1, cancelled=cancelled,
+                                   on_token=lambda ph, tok: calls.append(tok))
+        assert len(polls) == answer_false + 1  # no poll after the cancel
+        assert len(calls) == at_cancel[0], (answer_false, calls)  # no token after it
+        if answer_false < 5:
+            assert not calls
+    never = []
+    tokens, _, _ = engine.generate_tokens(prefix, sampling, 1,
+                                          cancelled=lambda: never.append(1) and False)
+    assert len(tokens) == 16 and len(never) >= 5 + 16
+    engine.close()
+
+
 def test_end_token_and_min_tokens_in_semantic_phase(yuear_lib):
     # Zero layers' weights make the final hidden state the normalised
     # embedding (all ones), so logits are the row sums of lm_head: only the

@@ -51,7 +51,18 @@ def test_cxx_facade_matches_python_binding(yuear_lib):
     assert cases["sampled"]["callback"] == sampled and cases["sampled"]["phase"] == "full"
     assert cases["cfg"]["tokens"] == cfg
     assert cases["invalid"]["error"] == "ValueError"
-    assert cases["cancelled"]["error"] == "InterruptedError" and cases["cancelled"]["calls"] == 3
+    # the reference's cancellation points and messages (sampling.cpp:156,
+    # 164, 206, 243): nothing is reported once a poll has seen the cancel
+    expect = {"cancel_before": ("Cancelled before prefill", 0, 1),
+              "cancel_branch1": ("Cancelled before prefill", 0, 4),
+              "cancel_prefill": ("Cancelled during prefill", 0, 5),
+              "cancelled": ("Cancelled during full", 3, None)}
+    for name, (message, calls, polls) in expect.items():
+        case = cases[name]
+        assert case["error"] == "InterruptedError", case
+        assert case["message"] == message and case["calls"] == calls, case
+        if polls is not None:
+            assert case["polls"] == polls, case
     assert cases["throwing"]["error"] == "out_of_range" and cases["throwing"]["what"] == "boom"
     assert cases["again"]["tokens"] == greedy
 

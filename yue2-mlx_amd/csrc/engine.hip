@@ -248,9 +248,12 @@ struct yuear_engine {
     if (rope_cos) (void)hipFree(rope_cos);
     if (tiled) (void)hipFree(tiled);
   }
-  void check_cancelled(const char *where) {
-    if (cancelled.load(std::memory_order_relaxed))
-      throw Error("InterruptedError", std::string("Cancelled during ") + where);
+  // Throws InterruptedError(message) when yuear_engine_cancel was called or
+  // the caller's poll (sampling.cpp:135-137 cancelled_at) says so.
+  void cancelled_at(const char *message, yuear_cancel_poll poll = nullptr,
+                    void *user = nullptr) {
+    if (cancelled.load(std::memory_order_relaxed) || (poll && poll(user) != 0))
+      throw Error("InterruptedError", message);
   }
 };
 
@@ -913,8 +916,11 @@ void check_tokens(const int32_t *ids, int n, int vocab) {  // sampling.cpp:139-1
       invalid("Token IDs must be in [0, " + std::to_string(vocab) + ")");
 }
 
-// prefill of one branch (sampling.cpp:152-183; ar.cpp:246-301 with T > 1)
-void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logits_out) {
+// prefill of one branch (sampling.cpp:152-183; ar.cpp:246-301 with T > 1).
+// Cancellation is polled before any work and between chunks (each chunk ends
+// in a stream synchronisation, so a poll falls between two chunks' work).
+void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logits_out,
+             yuear_cancel_poll poll = nullptr, void *poll_user = nullptr) {
   yuear_engine &E = *S.e;
   const Config &c = E.cfg;
   if (b < 0 || b >= S.B)
@@ -922,9 +928,10 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
   check_tokens(ids, n, c.V);
   if (S.host_pos[b] + n > S.cap)
     invalid("KV cache capacity exceeded; generation was not shortened");
+  E.cancelled_at("Cancelled before prefill", poll, poll_user);  // sampling.cpp:156
   hipStream_t st = S.stream;
   for (int start = 0; start < n; start += S.chunk) {
-    E.check_cancelled("prefill");
+    E.cancelled_at("Cancelled during prefill", poll, poll_user);  // sampling.cpp:164
     const int T = std::min(S.chunk, n - start);
     const int pos0 = S.host_pos[b];
     std::memcpy(S.pin_tok, ids + start, size_t(T) * 4);
@@ -1469,9 +1476,9 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
                                    const yuear_sampling *sampling, uint64_t seed,
                                    const char *phase_name, const int32_t *negative,
                                    int32_t n_negative, double cfg_scale, int32_t legacy_off,
-                                   yuear_token_callback on_token, void *user_data,
-                                   int32_t *tokens_out, int32_t *n_out, int32_t *truncated,
-                                   char **timing_json, char **error_json) {
+                                   yuear_cancel_poll cancel_poll, yuear_token_callback on_token,
+                                   void *user_data, int32_t *tokens_out, int32_t *n_out,
+                                   int32_t *truncated, char **timing_json, char **error_json) {
   if (n_out) *n_out = 0;
   if (timing_json) *timing_json = nullptr;
   return guarded(error_json, [&] {
@@ -1498,7 +1505,7 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
     }
     if (seed >= (uint64_t(1) << 63))
       invalid("seed must be an integer in [0, 2**63)");
-    E->check_cancelled("prefill");
+    E->cancelled_at("Cancelled before prefill", cancel_poll, user_data);  // sampling.cpp:206
     const int branches = cfg_scale != 1 ? 2 : 1;
     const int capacity =
         std::max(n_prefix, branches == 2 ? n_negative : 0) + s.max_tokens;
@@ -1509,9 +1516,9 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
     auto since = [&](clock::time_point t) {
       return std::chrono::duration<double>(clock::now() - t).count();
     };
-    prefill(*S, 0, prefix, n_prefix, nullptr);
+    prefill(*S, 0, prefix, n_prefix, nullptr, cancel_poll, user_data);
     if (branches == 2)
-      prefill(*S, 1, negative, n_negative, nullptr);
+      prefill(*S, 1, negative, n_negative, nullptr, cancel_poll, user_data);
     HIPC(hipStreamSynchronize(S->stream));
     const double prefill_seconds = since(t0);
 
@@ -1558,7 +1565,19 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
     double ttft = -1.0;
     bool eos = false, cancelled = false;
     int count = 0, launched = 0, consumed = 0;
+    // The reference polls at the start of every step, before that step's
+    // token is drawn and reported (sampling.cpp:243): here token i is
+    // reported only after a poll that follows token i - 1's report, and
+    // nothing is launched or reported once a poll has seen the cancel.
+    auto poll = [&]() {
+      if (!cancelled && (E->cancelled.load(std::memory_order_relaxed) ||
+                         (cancel_poll && cancel_poll(user_data) != 0)))
+        cancelled = true;
+      return cancelled;
+    };
     auto consume = [&]() {
+      if (poll())
+        return;
       HIPC(hipEventSynchronize(ev[consumed % kDepth]));
       const int token = S->pin_tok[consumed];
       ++consumed;
@@ -1573,10 +1592,8 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
       tokens_out[count++] = token;
     };
     while (launched < s.max_tokens && !eos) {
-      if (E->cancelled.load(std::memory_order_relaxed)) {
-        cancelled = true;
+      if (poll())
         break;
-      }
       if (launched + 1 < s.max_tokens)
         HIPC(hipGraphLaunch(exec, S->stream));  // sample + forward
       else
@@ -1586,6 +1603,8 @@ yuear_status yuear_generate_tokens(yuear_engine *E, const int32_t *prefix, int32
       ++launched;
       if (launched - consumed >= kDepth - 1)
         consume();
+      if (cancelled)
+        break;
     }
     while (consumed < launched && !eos && !cancelled)
       consume();

@@ -63,6 +63,7 @@ class SongRequestC(C.Structure):
 
 
 TOKEN_CB = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_int32)
+CANCEL_POLL = C.CFUNCTYPE(C.c_int32, C.c_void_p)
 
 lib = C.CDLL(LIB_PATH)
 _P = C.POINTER
@@ -85,7 +86,8 @@ _SIGS = {
     "yuear_rope_table": (None, [C.c_int32, C.c_int32, C.c_double, u16p, u16p]),
     "yuear_generate_tokens": (C.c_int, [C.c_void_p, i32p, C.c_int32, _P(SamplingC), C.c_uint64,
                                         C.c_char_p, i32p, C.c_int32, C.c_double, C.c_int32,
-                                        TOKEN_CB, C.c_void_p, i32p, i32p, i32p, _P(C.c_void_p),
+                                        CANCEL_POLL, TOKEN_CB, C.c_void_p, i32p, i32p, i32p,
+                                        _P(C.c_void_p),
                                         _P(C.c_void_p)]),
     "yuear_session_begin": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_char_p,
                                       _P(C.c_void_p), _P(C.c_void_p)]),
@@ -461,8 +463,11 @@ class Engine:
         return Session(self, branches, capacity, phase)
 
     def generate_tokens(self, prefix, sampling, seed, phase="full", negative=None, cfg_scale=1.0,
-                        legacy_off=False, on_token=None):
-        """sampling.cpp:185-288 -> (tokens, timing, truncated)."""
+                        legacy_off=False, on_token=None, cancelled=None):
+        """sampling.cpp:185-288 -> (tokens, timing, truncated). `cancelled`: a
+        predicate polled where the reference calls cancelled_at (before each
+        prefill, between prefill chunks, before each token); a cancelled run
+        raises InterruptedError with the reference's message."""
         pre = _i32(prefix)
         neg = _i32(negative) if negative is not None else np.zeros(0, dtype=np.int32)
         s = sampling_struct(sampling)
@@ -482,11 +487,22 @@ class Engine:
                 failure.append(exc)
                 self.cancel()
 
+        def _poll(_user):
+            if failure:
+                return 1
+            try:
+                return 1 if cancelled is not None and cancelled() else 0
+            except BaseException as exc:  # a throwing predicate cancels too
+                failure.append(exc)
+                return 1
+
         cb = TOKEN_CB(_cb)
+        poll = CANCEL_POLL(_poll) if cancelled is not None else CANCEL_POLL()
         status = lib.yuear_generate_tokens(
             self.handle, pre.ctypes.data_as(i32p), pre.size, C.byref(s), int(seed),
             phase.encode(), neg.ctypes.data_as(i32p) if neg.size else None, neg.size,
-            float(cfg_scale), int(legacy_off), cb, None, out.ctypes.data_as(i32p), C.byref(n),
+            float(cfg_scale), int(legacy_off), poll, cb, None, out.ctypes.data_as(i32p),
+            C.byref(n),
             C.byref(trunc), C.byref(timing), C.byref(err))
         if failure:
             if err.value:
