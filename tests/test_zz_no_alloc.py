@@ -40,7 +40,9 @@ def bf(x):
     return cpu_ref.f32_to_bf16(np.asarray(x, dtype=np.float32))
 
 
-def run(torch, yuear_lib, fn, heads, kv, batch_pos, splits, seed):
+def inputs(torch, yuear_lib, heads, kv, batch_pos, seed):
+    """Device arguments of one decode attention call (qkv, norms, rope
+    tables, K, blocked V, positions, output) and the capacity."""
     rng = np.random.default_rng(seed)
     B = len(batch_pos)
     cap = yuear_lib.kv_slots(max(batch_pos) + 9)
@@ -52,10 +54,19 @@ def run(torch, yuear_lib, fn, heads, kv, batch_pos, splits, seed):
     a = [dev(torch, t) for t in (qkv, qn, kn, cos, sin, k, yuear_lib.v_blocked(v))]
     dpos = dev(torch, np.array(batch_pos, np.int32))
     out = dev(torch, np.zeros((B, heads * 128), np.uint16))
-    rc = fn(a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), 1e-5, a[3].data_ptr(),
-            a[4].data_ptr(), a[5].data_ptr(), a[6].data_ptr(), dpos.data_ptr(), heads, kv, cap,
-            B, splits, out.data_ptr(), None)
-    return rc, host(torch, out), host(torch, a[5]), host(torch, a[6])
+    return a + [dpos, out], cap
+
+
+def call(fn, a, heads, kv, cap, batch, splits):
+    return fn(a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), 1e-5, a[3].data_ptr(),
+              a[4].data_ptr(), a[5].data_ptr(), a[6].data_ptr(), a[7].data_ptr(), heads, kv, cap,
+              batch, splits, a[8].data_ptr(), None)
+
+
+def run(torch, yuear_lib, fn, heads, kv, batch_pos, splits, seed):
+    a, cap = inputs(torch, yuear_lib, heads, kv, batch_pos, seed)
+    rc = call(fn, a, heads, kv, cap, len(batch_pos), splits)
+    return rc, host(torch, a[8]), host(torch, a[5]), host(torch, a[6])
 
 
 @pytest.mark.parametrize("first,second", [
@@ -78,14 +89,17 @@ def test_noalloc_matches_allocating_entry_twice(torch, yuear_lib, first, second)
 def test_noalloc_allocates_nothing_after_set_up(torch, yuear_lib):
     fn = yuear_lib.lib.yuear_op_attention_decode_noalloc
     assert run(torch, yuear_lib, fn, 24, 8, [200], 8, seed=5)[0] == 0  # set-up call
+    # every input and output exists before the window: between the two
+    # readings only the entry point runs (twice), so any device allocation
+    # it made would lower the free memory
+    a, cap = inputs(torch, yuear_lib, 24, 8, [100, 900], seed=6)
     torch.cuda.synchronize()
     free0, _ = torch.cuda.mem_get_info()
-    assert run(torch, yuear_lib, fn, 24, 8, [100], 4, seed=6)[0] == 0
+    assert call(fn, a, 24, 8, cap, 2, 4) == 0
+    assert call(fn, a, 24, 8, cap, 2, 12) == 0
     torch.cuda.synchronize()
     free1, _ = torch.cuda.mem_get_info()
-    # the inputs of run() are torch tensors freed to torch's cache, which
-    # mem_get_info does not see returned; the entry point itself adds nothing
-    assert free1 >= free0 - (64 << 20)
+    assert free1 == free0, (free0, free1)
 
 
 def test_noalloc_refuses_layouts_beyond_its_scratch(torch, yuear_lib):
