@@ -111,6 +111,12 @@ def prep_qk(oracle, raw, gain, pos, theta=5e5):
     (24, 8, [4095], 1), (24, 8, [777], 7), (16, 8, [300], 32), (4, 2, [50], 8),
     (24, 8, [513, 1535], 32), (24, 8, [100, 1200, 7, 2047, 64, 500, 9, 1000], 32),
     (24, 8, [8191], 64),  # KV 8192: one launch of the long-context decode
+    # every other accepted heads-per-kv-head ratio: G = 1 (one head per wave
+    # in the prologue), 4, 6 and 8 (two and three heads per wave)
+    (8, 8, [15], 64), (8, 8, [300, 4095], 32),
+    (32, 8, [15], 64), (32, 8, [777], 7), (32, 8, [4095], 33),
+    (48, 8, [16], 64), (48, 8, [1000, 63], 24),
+    (64, 8, [15], 64), (64, 8, [2047], 16), (64, 8, [4095], 1),
 ])
 def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_heads, batch_pos,
                                          splits):

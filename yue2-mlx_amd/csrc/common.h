@@ -164,14 +164,20 @@ __device__ __forceinline__ float row_max16(float v) {
 // b. With a = b = v on entry:
 //   permlane16: a = rows (0,0,2,2) of v, b = rows (1,1,3,3);
 //   permlane32: a = low half twice,     b = high half twice.
-// Issued through inline asm with both operands read-write: this compiler's
-// two-result builtins lose the second result when both are added together.
-// The two wait states before match what the compiler emits for the builtin.
+// Through the compiler builtins, so that its hazard recognizer sees the
+// instruction (gfx950: two wait states after a VALU write of an operand,
+// four after a v_cmpx write of exec) and schedules around it. The two
+// results are read as plain element values (a bit cast of a vector element
+// lvalue reads element 0 with this clang; see as_bf16x2 below).
 __device__ __forceinline__ void permlane16_swap(uint32_t &a, uint32_t &b) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
 }
 __device__ __forceinline__ void permlane32_swap(uint32_t &a, uint32_t &b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
 }
 __device__ __forceinline__ float sum_row_pairs(float v) {  // rows 2k + 2k+1
   uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
