@@ -197,6 +197,34 @@ def run_long(args, engine, c):
             "mfma_frac": round(flops / pre_s / PEAK_BF16, 4), "decode_curve": curve}
 
 
+def run_prefill(args, engine, c):
+    """Profiling mode: `--prefills` 3000-token prefills of the 3B model (the
+    prefill half of the long-context workload), timed one by one."""
+    import numpy as np
+    import torch
+    T = 3000
+    rng = np.random.default_rng(args.seed + 4)
+    times = []
+    for i in range(args.prefills + 1):  # the first call loads code objects
+        s = engine.session(1, T + 8)
+        prompt = rng.integers(0, c["vocab_size"], size=T).tolist()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        s.prefill(0, prompt)
+        torch.cuda.synchronize()
+        if i:
+            times.append(time.perf_counter() - t)
+        s.close()
+        log(f"[bench] prefill {i}: {(time.perf_counter() - t) * 1e3:.2f} ms")
+    flops = prefill_flops(c, T)
+    best = min(times)
+    return {"metric": "prefill TFLOP/s (3000 tokens)", "value": round(flops / best / 1e12, 2),
+            "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+            "data": "synthetic", "config": {"workload": "3B decoder, 3000-token prefill"},
+            "prefill_ms": [round(t * 1e3, 3) for t in times], "prefill_flops": flops,
+            "mfma_frac": round(flops / best / PEAK_BF16, 4)}
+
+
 def run_nar(args):
     """The acoustic-model attention (nar_attention.cpp:63-218) at the 3B head
     shape: a 512-frame chunk attending over 3000 conditioning keys plus its
@@ -307,11 +335,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-launches", type=int, default=112)
-    ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8", "nar"),
+    ap.add_argument("--prefills", type=int, default=3,
+                    help="--config prefill: number of timed 3000-token prefills")
+    ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8", "nar", "prefill"),
                     default="decode",
                     help="workload (decode: the headline batch-1 KV-4096 line)")
     ap.add_argument("--kernel-only", default=None,
-                    help="profiling mode: only time this decode kernel (e.g. gate_up)")
+                    help="profiling mode: only time these decode kernels, comma-separated "
+                         "(qkv, attention, o_proj, gate_up, down, lm_head), in that order")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="profiling mode: one device-to-device copy of MIB MiB (counter scale)")
     args = ap.parse_args()
@@ -348,7 +379,8 @@ def main():
     log(f"[bench] weights ready {time.perf_counter() - t_start:.1f}s; uploading")
     engine = yuear.Engine(c, weights, bits=bits)
     if args.config != "decode":
-        line = {"cfg": run_cfg, "long": run_long, "batch8": run_batch8}[args.config](
+        line = {"cfg": run_cfg, "long": run_long, "batch8": run_batch8,
+                "prefill": run_prefill}[args.config](
             args, engine, c)
         print(json.dumps(line), flush=True)
         log(f"[bench] total {time.perf_counter() - t_start:.1f}s")
@@ -362,9 +394,10 @@ def main():
     if args.kernel_only:
         # the decode line's prompt length, so the attention reads its KV length
         session.prefill(0, rng.integers(0, c["vocab_size"], size=prefill).tolist())
-        ms = session.time_kernel(args.kernel_only, args.kernel_launches)
-        print(json.dumps({"kernel": args.kernel_only, "launches": args.kernel_launches,
-                          "us": ms * 1e3}), flush=True)
+        for name in args.kernel_only.split(","):
+            ms = session.time_kernel(name, args.kernel_launches)
+            print(json.dumps({"kernel": name, "launches": args.kernel_launches,
+                              "us": ms * 1e3}), flush=True)
         return
     prompt = rng.integers(0, c["vocab_size"], size=prefill).tolist()
     t = time.perf_counter()
