@@ -75,15 +75,18 @@ __device__ __forceinline__ void gemv_block(const GemvParams &p, int blk, u32x4 *
     }
   }
 
-  // 3. Stage activations (gather copy-out, RMSNorm) into LDS.
+  // 3. Stage activations (gather copy-out, RMSNorm) into LDS. Every one of
+  // the B template rows is processed without a branch on p.batch (rows past
+  // it repeat the last real row and are never read back), so the rows'
+  // reduction and normalisation chains interleave instead of running one
+  // after the other (batch 2: 0.8-0.9 us less per normed launch on MI355X).
   float ss[B];
 #pragma unroll
   for (int b = 0; b < B; ++b) {
     ss[b] = 0.f;
-    if (b >= p.batch)
-      continue;
-    const uint16_t *src = p.embed ? p.embed + size_t(gemv_token_row(p, b)) * p.k
-                                  : p.x + size_t(b) * p.x_stride;
+    const int bb = min(b, p.batch - 1);
+    const uint16_t *src = p.embed ? p.embed + size_t(gemv_token_row(p, bb)) * p.k
+                                  : p.x + size_t(bb) * p.x_stride;
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int c = threadIdx.x + 256 * i;
@@ -94,7 +97,7 @@ __device__ __forceinline__ void gemv_block(const GemvParams &p, int blk, u32x4 *
         v = xr[b][i];
       else
         v = reinterpret_cast<const u32x4 *>(src)[c];
-      if (p.x_out && blk == 0)
+      if (p.x_out && blk == 0 && b < p.batch)
         reinterpret_cast<u32x4 *>(p.x_out + size_t(b) * p.x_stride)[c] = v;
       if (p.norm_w) {
         const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
@@ -119,12 +122,11 @@ __device__ __forceinline__ void gemv_block(const GemvParams &p, int blk, u32x4 *
     __syncthreads();
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      if (b >= p.batch)
-        continue;
       const float total = (red[b][0] + red[b][1]) + (red[b][2] + red[b][3]);
       const float scale = rbf(1.0f / __builtin_sqrtf(total / float(p.k) + p.eps));
-      const uint16_t *src = p.embed ? p.embed + size_t(gemv_token_row(p, b)) * p.k
-                                    : p.x + size_t(b) * p.x_stride;
+      const int bb = min(b, p.batch - 1);
+      const uint16_t *src = p.embed ? p.embed + size_t(gemv_token_row(p, bb)) * p.k
+                                    : p.x + size_t(bb) * p.x_stride;
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
         const int c = threadIdx.x + 256 * i;
