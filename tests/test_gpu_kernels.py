@@ -68,6 +68,8 @@ GEMV_CASES = [  # (n, k, batch, norm, epilogue)
     (998, 3072, 5, True, 2),
     (5110, 3072, 8, False, 0),    # last 16-row block partly past n
     (4100, 3072, 3, True, 1),     # 257 blocks: one past a 256-CU grid, residual epilogue
+    (2048, 6144, 4, True, 0),     # 16-wave forms with the RMSNorm prologue
+    (1024, 8192, 8, True, 2),
     (96, 512, 1, False, 2),
 ]
 
