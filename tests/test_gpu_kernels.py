@@ -280,9 +280,9 @@ def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residua
 
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])
 def test_gemm_split_k_is_deterministic(torch, yuear_lib, m, n, k):
-    """Shapes whose tiles fill less than a round of CUs split K over several
-    workgroups; the partials are summed in K order whichever workgroup
-    arrives last, so repeated launches give identical bits."""
+    """Every output sums its K products in the same order on each launch
+    (no split of K across workgroups, no atomics), so repeated launches of
+    narrow, wide and deep shapes give identical bits."""
     rng = np.random.default_rng(m + 3 * n)
     a = dev(torch, bf(rng.normal(size=(m, k))))
     w = dev(torch, bf(rng.normal(size=(n, k)) * 0.02))
