@@ -298,8 +298,8 @@ int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                       int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                       int32_t ldc, int32_t residual, void *stream);
 /* Test hook (no counterpart in the reference): yuear_op_gemm with its tile
- * shape forced instead of chosen, shape 0..4 = 256x256, 256x128, 128x256,
- * 256x192, 128x128; other values return hipErrorInvalidValue (1). */
+ * shape forced instead of chosen, shape 0..5 = 256x256, 256x128, 128x256,
+ * 256x192, 128x128, 192x192; other values return hipErrorInvalidValue (1). */
 int32_t yuear_op_gemm_tile(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                            int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                            int32_t ldc, int32_t residual, int32_t shape, void *stream);

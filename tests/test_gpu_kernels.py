@@ -235,7 +235,7 @@ def test_gemm_prefill_shapes(torch, yuear_lib, oracle, m, n, k, residual):
     assert_close_bf16(got[rows], ref, scale=scale, exact_frac=0.9)
 
 
-@pytest.mark.parametrize("shape", range(5))
+@pytest.mark.parametrize("shape", range(6))
 @pytest.mark.parametrize("m,n,k", [(300, 1000, 512), (3000, 16384, 3072), (5, 36, 64)])
 def test_gemm_swiglu_epilogue(torch, yuear_lib, oracle, shape, m, n, k):
     """The SwiGLU form (residual = 2) on interleaved gate/up rows against the
@@ -258,10 +258,10 @@ def test_gemm_swiglu_epilogue(torch, yuear_lib, oracle, shape, m, n, k):
                                             dc.data_ptr(), n // 2, 2, shape, None) == 1
 
 
-@pytest.mark.parametrize("shape", range(5))
+@pytest.mark.parametrize("shape", range(6))
 @pytest.mark.parametrize("m,n,k,residual", [(300, 1000, 512, 0), (517, 776, 192, 1), (1, 200, 64, 1)])
 def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residual):
-    """Each of the five tile shapes, forced, on ragged sizes (M and N not
+    """Each of the six tile shapes, forced, on ragged sizes (M and N not
     multiples of any tile, N not a multiple of 8, single-row M)."""
     rng = np.random.default_rng(m + n + shape)
     a = bf(rng.normal(size=(m, k)))
@@ -275,7 +275,7 @@ def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residua
     scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
     assert_close_bf16(host(torch, dc), ref, scale=scale, exact_frac=0.9)
     assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n, k,
-                                            dc.data_ptr(), n, residual, 5, None) == 1
+                                            dc.data_ptr(), n, residual, 6, None) == 1
 
 
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])

@@ -31,11 +31,13 @@
 //
 // Tile shapes (launch_gemm picks the one with the least estimated time for
 // the shape and the CU count): 256 x 256 (8 waves of 128 x 64), 256 x 128 and
-// 128 x 256 (8 waves of 64 x 64), 256 x 192 (8 waves of 64 x 96) and
-// 128 x 128 (4 waves of 64 x 64, two workgroups per CU); the first three on
-// 16 x 16 x 32 MFMAs (gemm_tile16 below), the others on 32 x 32 x 16. At the 3B prefill
-// shapes (M = 3000) QKV and gate/up take 256 x 256 tiles, the output and down
-// projections (N = 3072, 144 such tiles for 256 CUs) 256 x 192.
+// 128 x 256 (8 waves of 64 x 64), 256 x 192 (8 waves of 64 x 96), 192 x 192
+// (8 waves of 96 x 48) and 128 x 128 (4 waves of 64 x 64, two workgroups per
+// CU); all but the last on 16 x 16 x 32 MFMAs (gemm_tile16 below), that one
+// on 32 x 32 x 16. At the 3B prefill shapes (M = 3000) QKV and gate/up take
+// 256 x 256 tiles, the output and down projections (N = 3072) 192 x 192:
+// 256 tiles for 256 CUs where 256 x 192 leaves 64 CUs idle (down 148 -> 131
+// us, o_proj 61 -> 52).
 #include <algorithm>
 
 #include "common.h"
@@ -286,6 +288,7 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
   constexpr int ABLK = BM / 8, BLK = (BM + BN) / 8;
   constexpr int BPW = BLK / NW;
   constexpr int STAGE = (BM + BN) * 128;
+  static_assert(BPW * NW == BLK && TM * WM * 16 == BM && TN * WN * 16 == BN, "tile shape");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -415,14 +418,15 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
   __global__ __launch_bounds__(WM * WN * 64) void NAME(GemmParams p, int tiles_n) { \
     BODY<BM, BN, WM, WN>(p, tiles_n);                                            \
   }
-// MFMA form per shape, as measured: 16 x 16 x 32 for 256 x 256, 256 x 128
-// and 128 x 256; 32 x 32 x 16 for 256 x 192 and 128 x 128 (their 16 x 16
-// forms were equal or slower).
+// MFMA form per shape, as measured: 16 x 16 x 32 for all but 128 x 128
+// (256 x 192 on it 2-4% faster than on 32 x 32 x 16 once its fragment reads
+// were conflict-free; 128 x 128 6-10% slower).
 YUEAR_GEMM_KERNEL(gemm_256x256, gemm_tile16, 256, 256, 2, 4)
 YUEAR_GEMM_KERNEL(gemm_256x128, gemm_tile16, 256, 128, 4, 2)
 YUEAR_GEMM_KERNEL(gemm_128x256, gemm_tile16, 128, 256, 2, 4)
-YUEAR_GEMM_KERNEL(gemm_256x192, gemm_tile, 256, 192, 4, 2)
+YUEAR_GEMM_KERNEL(gemm_256x192, gemm_tile16, 256, 192, 4, 2)
 YUEAR_GEMM_KERNEL(gemm_128x128, gemm_tile, 128, 128, 2, 2)
+YUEAR_GEMM_KERNEL(gemm_192x192, gemm_tile16, 192, 192, 2, 4)
 #undef YUEAR_GEMM_KERNEL
 
 // Time model of the tile shapes, in microseconds per 48 K steps measured on
@@ -435,8 +439,8 @@ struct TileShape {
 };
 constexpr TileShape kShapes[] = {
     {256, 256, 1, 63.0, 85.0, 85.0}, {256, 128, 1, 43.5, 50.0, 50.0},
-    {128, 256, 1, 44.3, 50.0, 50.0}, {256, 192, 1, 50.5, 60.0, 60.0},
-    {128, 128, 2, 34.3, 40.0, 50.8},
+    {128, 256, 1, 44.3, 50.0, 50.0}, {256, 192, 1, 49.0, 58.0, 58.0},
+    {128, 128, 2, 34.3, 40.0, 50.8}, {192, 192, 1, 41.0, 49.0, 49.0},
 };
 
 template <int BM, int BN, int WM, int WN>
@@ -496,6 +500,7 @@ hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s) {
   case 2: return launch_tile<128, 256, 2, 4>(gemm_128x256, p, s);
   case 3: return launch_tile<256, 192, 4, 2>(gemm_256x192, p, s);
   case 4: return launch_tile<128, 128, 2, 2>(gemm_128x128, p, s);
+  case 5: return launch_tile<192, 192, 2, 4>(gemm_192x192, p, s);
   }
   return hipErrorInvalidValue;
 }

@@ -182,7 +182,7 @@ struct GemmParams {
 };
 // MFMA GEMM (gemm.hip); k a multiple of 64, lda a multiple of 8. No scratch.
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
-// One of the GEMM's tile shapes (0..4, see gemm.hip) and the shape
+// One of the GEMM's tile shapes (0..5, see gemm.hip) and the shape
 // launch_gemm would pick for m x n on `cus` CUs.
 hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s);
 int gemm_tile_choice(int m, int n, int cus);
