@@ -72,56 +72,76 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const uint16_t *x, i
 
 
 // q/k RMSNorm + RoPE for T tokens, K/V append (ar.cpp:268-282).
-// One workgroup per token; wave w takes heads w, w + 4, ... and issues the
-// loads of up to 8 of them before the first reduction, so each wave keeps
-// several independent loads in flight (the per-head work is a short
-// dependent chain: load, cross-lane sum, rotate, store). Workgroup i runs on
-// XCD i mod 8: token t = (i mod 8) * per + i / 8 keeps runs of consecutive
-// tokens on one XCD, so the 2-byte V stores of neighbouring slots (one
-// 64-byte block column per dim) merge in that XCD's L2 before write-back.
-__global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p, int per) {
-  constexpr int kBatch = 8;
-  const int t = int(blockIdx.x % 8) * per + int(blockIdx.x / 8);
-  if (t >= p.tokens)
-    return;
+// Workgroup (block, head): the positions of one 32-key cache block (the
+// block layout's unit) that this call covers, for one head (q heads, then
+// k heads, then v heads); wave w takes the block's positions 8w .. 8w + 7
+// and issues all 8 row loads (256 bytes each) before the first reduction.
+// q / k rows: RMSNorm + RoPE per row (a short dependent chain: cross-lane
+// sum, rotate), stored row-major. V rows: staged in LDS, then written as the
+// block's dim-major rows (64 bytes of 32 keys per dim) in 16-byte pieces;
+// keys of a partly covered block outside the call's positions keep their
+// cache contents (2-byte stores for those pieces only).
+__global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
+  __shared__ uint32_t vrow[attn::kBlock][65];  // V tile: [key in block][dim pair], padded
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int pos = p.pos0 + t;
-  const uint32_t *row = reinterpret_cast<const uint32_t *>(p.qkv + size_t(t) * p.qkv_stride);
-  NormRope rq, rk;
-  load_rope(rq, p.rope_cos + size_t(pos) * 64, p.rope_sin + size_t(pos) * 64, lane);
-  rk = rq;
-  if (p.q_norm)
-    load_gain(rq, p.q_norm, lane);
-  if (p.k_norm)
-    load_gain(rk, p.k_norm, lane);
-  const int nh = p.heads + 2 * p.kv_heads;
-  for (int h0 = wave; h0 < nh; h0 += 4 * kBatch) {
-    uint32_t pair[kBatch];
+  const int h = blockIdx.y;
+  const int blk = p.pos0 / attn::kBlock + int(blockIdx.x);
+  const int lo = max(blk * attn::kBlock, p.pos0);
+  const int hi = min(blk * attn::kBlock + attn::kBlock, p.pos0 + p.tokens);  // positions [lo, hi)
+  const int base = blk * attn::kBlock + 8 * wave;
+  uint32_t v[8];
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j)
-      pair[j] = row[size_t(min(h0 + 4 * j, nh - 1)) * 64 + lane];
+  for (int j = 0; j < 8; ++j) {  // clamped rows: always a valid address
+    const int t = min(max(base + j, lo), hi - 1) - p.pos0;
+    v[j] = reinterpret_cast<const uint32_t *>(p.qkv + size_t(t) * p.qkv_stride)[h * 64 + lane];
+  }
+  if (h < p.heads + p.kv_heads) {
+    const bool is_q = h < p.heads;
+    const uint16_t *gain = is_q ? p.q_norm : p.k_norm;
+    NormRope r;
+    if (gain)
+      load_gain(r, gain, lane);
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int h = h0 + 4 * j;  // uniform per wave
-      if (h >= nh)
-        break;
-      float y0 = bflo(pair[j]), y1 = bfhi(pair[j]);
-      uint32_t *dst;
-      if (h < p.heads) {
-        norm_rope_apply(y0, y1, p.q_norm != nullptr, p.eps, rq, lane, y0, y1);
-        dst = reinterpret_cast<uint32_t *>(p.q_out + (size_t(t) * p.heads + h) * 128);
-      } else if (h < p.heads + p.kv_heads) {
-        const int kvh = h - p.heads;
-        norm_rope_apply(y0, y1, p.k_norm != nullptr, p.eps, rk, lane, y0, y1);
-        dst = reinterpret_cast<uint32_t *>(p.k_cache + (size_t(kvh) * p.capacity + pos) * 128);
-      } else {  // V: dims 2 lane, 2 lane + 1 into the slot's 32-key block column
-        const int kvh = h - p.heads - p.kv_heads;
-        uint16_t *vh = p.v_cache + size_t(kvh) * p.capacity * 128;
-        vh[attn::v_index(pos, 2 * lane)] = f2bf(y0);
-        vh[attn::v_index(pos, 2 * lane + 1)] = f2bf(y1);
+    for (int j = 0; j < 8; ++j) {
+      const int pos = base + j;
+      if (pos < lo || pos >= hi)  // uniform per wave
         continue;
-      }
+      load_rope(r, p.rope_cos + size_t(pos) * 64, p.rope_sin + size_t(pos) * 64, lane);
+      float y0, y1;
+      norm_rope_apply(bflo(v[j]), bfhi(v[j]), gain != nullptr, p.eps, r, lane, y0, y1);
+      uint32_t *dst =
+          is_q ? reinterpret_cast<uint32_t *>(p.q_out + (size_t(pos - p.pos0) * p.heads + h) * 128)
+               : reinterpret_cast<uint32_t *>(p.k_cache +
+                                              (size_t(h - p.heads) * p.capacity + pos) * 128);
       dst[lane] = uint32_t(f2bf(y0)) | (uint32_t(f2bf(y1)) << 16);
+    }
+    return;
+  }
+  // V: [key][dim pair] into LDS, then piece (d, c) = keys 8c .. 8c + 7 of dim d
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    vrow[8 * wave + j][lane] = v[j];
+  __syncthreads();
+  uint16_t *vh = p.v_cache + size_t(h - p.heads - p.kv_heads) * p.capacity * 128;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int piece = int(threadIdx.x) + 256 * i;  // 512 pieces: 128 dims x 4
+    const int d = piece >> 2, c = piece & 3;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t a = vrow[8 * c + 2 * e][d >> 1], b2 = vrow[8 * c + 2 * e + 1][d >> 1];
+      w[e] = (d & 1) ? ((a >> 16) | (b2 & 0xffff0000u)) : ((a & 0xffffu) | (b2 << 16));
+    }
+    const int k0 = blk * attn::kBlock + 8 * c;
+    uint16_t *dst = vh + attn::v_index(k0, d);
+    if (k0 >= lo && k0 + 8 <= hi) {
+      *reinterpret_cast<u32x4 *>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (k0 + e >= lo && k0 + e < hi)
+          dst[e] = uint16_t(w[e >> 1] >> (16 * (e & 1)));
     }
   }
 }
@@ -185,8 +205,8 @@ hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
   if (p.head_dim != 128 || p.tokens < 1 || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity ||
       p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
-  const int per = (p.tokens + 7) / 8;
-  hipLaunchKernelGGL(qk_prep_kernel, dim3(8 * per), dim3(256), 0, s, p, per);
+  const int blocks = (p.pos0 + p.tokens - 1) / attn::kBlock - p.pos0 / attn::kBlock + 1;
+  hipLaunchKernelGGL(qk_prep_kernel, dim3(blocks, p.heads + 2 * p.kv_heads), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
