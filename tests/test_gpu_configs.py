@@ -1,4 +1,4 @@
-"""The north-star workloads of the 3B decoder on the GPU against the oracle.
+"""The benchmark workloads of the 3B decoder on the GPU against the oracle.
 
 Model: 28 layers, hidden 3072, 24/8 heads, FFN 8192, vocab 83968, N(0, 0.02)
 weights with unit norm gains (the bench's model). Each test runs one workload
@@ -79,12 +79,12 @@ def argmax_flips(a, b):
     return [i for i, (x, y) in enumerate(zip(a, b)) if int(np.argmax(x)) != int(np.argmax(y))]
 
 
-def test_cfg2_prefill_256_greedy_400(pair):
+def test_prefill_256_greedy_400(pair):
     engine, model, oracle = pair
     rng = np.random.default_rng(2002)
     prompt = rng.integers(0, V, size=256).tolist()
     n, n64 = 400, 100
-    print("[cfg2] oracle prefill 256 + 400 greedy steps", flush=True)
+    print("[greedy-400] oracle prefill 256 + 400 greedy steps", flush=True)
     cache = model.cache(256 + n)
     logits = model.prefill(prompt, cache)
     o_tokens, o_logits = [], []
@@ -93,7 +93,7 @@ def test_cfg2_prefill_256_greedy_400(pair):
         o_tokens.append(int(np.argmax(o_logits[-1])))  # greedy: lowest index on ties
         if i + 1 < n:
             logits = model.step(o_tokens[-1], cache)
-    print(f"[cfg2] fp64-accumulating oracle teacher-forced over the first {n64} steps",
+    print(f"[greedy-400] fp64-accumulating oracle teacher-forced over the first {n64} steps",
           flush=True)
     d_logits = []
     oracle.lib().oracle_set_accumulation(1)
@@ -104,12 +104,12 @@ def test_cfg2_prefill_256_greedy_400(pair):
             d_logits.append(f32(oracle, model.step(t, cache64)))
     finally:
         oracle.lib().oracle_set_accumulation(0)
-    print("[cfg2] GPU teacher-forced steps", flush=True)
+    print("[greedy-400] GPU teacher-forced steps", flush=True)
     s = engine.session(1, 256 + n)
     g_logits = [f32(oracle, s.prefill(0, prompt))] + [f32(oracle, s.step(t)[0])
                                                         for t in o_tokens[:-1]]
     s.close()
-    print("[cfg2] GPU free-running greedy stream (device sampler)", flush=True)
+    print("[greedy-400] GPU free-running greedy stream (device sampler)", flush=True)
     greedy = dict(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.0,
                   penalty_window=50, min_tokens=0, max_tokens=n)
     g_tokens, timing, _ = engine.generate_tokens(prompt, greedy, 0)
@@ -134,7 +134,7 @@ def test_cfg2_prefill_256_greedy_400(pair):
         dist[name] = dict(max_abs=float(np.abs(diff).max()), rms=float(np.sqrt(np.mean(diff ** 2))),
                           one_minus_cos=float(np.max(1 - cos)),
                           within=float(np.mean(np.abs(diff) <= 2e-2 + 1e-2 * np.abs(D))))
-    print(f"[cfg2] greedy-token flips against the fp64 oracle over {n64} steps: GPU "
+    print(f"[greedy-400] greedy-token flips against the fp64 oracle over {n64} steps: GPU "
           f"{len(flips_gpu)} {flips_gpu}, fp32 oracle {len(flips_ref)} {flips_ref}; GPU against "
           f"the fp32 oracle over {n} steps: {len(flips_32)} {flips_32[:12]}; distances to the fp64 "
           f"oracle {dist}; free-running stream first divergence {first}; "
@@ -157,7 +157,7 @@ def test_cfg2_prefill_256_greedy_400(pair):
         assert not flips_32
 
 
-def test_cfg3_cfg_pair_1024_sampled(pair):
+def test_cfg_pair_1024_sampled(pair):
     engine, model, oracle = pair
     rng = np.random.default_rng(2003)
     cond = rng.integers(0, V, size=512).tolist()
@@ -186,7 +186,7 @@ def test_cfg3_cfg_pair_1024_sampled(pair):
         if step < stretch:
             g_step[step] = logits
     assert len(set(tokens)) > 50  # a sampled stream, not a repeated token
-    print(f"[cfg3] {n} sampled tokens identical to the oracle's draws", flush=True)
+    print(f"[cfg-pair] {n} sampled tokens identical to the oracle's draws", flush=True)
     # a stretch after the prefill: the oracle decodes from the GPU's prefill
     # cache with the same tokens
     for b in range(2):
@@ -211,7 +211,7 @@ def test_cfg3_cfg_pair_1024_sampled(pair):
     s.close()
 
 
-def test_cfg4_prefill_3000_decode_to_kv_8192(pair):
+def test_prefill_3000_decode_to_kv_8192(pair):
     engine, model, oracle = pair
     rng = np.random.default_rng(2004)
     prompt = rng.integers(0, V, size=3000).tolist()
@@ -220,7 +220,7 @@ def test_cfg4_prefill_3000_decode_to_kv_8192(pair):
     s = engine.session(1, 8200)
     s.prefill(0, prompt)
     steps = 8191 - 3000
-    print(f"[cfg4] {steps} device-side greedy steps to KV 8191", flush=True)
+    print(f"[prefill-3000] {steps} device-side greedy steps to KV 8191", flush=True)
     _, toks = s.time_generate(greedy, 0, steps, reset=True)
     assert s.position(0) == 8191
     kv = [s.read_kv(layer, 0, 8191) for layer in range(LAYERS)]
@@ -231,7 +231,7 @@ def test_cfg4_prefill_3000_decode_to_kv_8192(pair):
     check_fidelity(gpu, ref[0], ref[1])
 
 
-def test_cfg5_batch8_prompts_128_to_2048_capacity_6144(pair):
+def test_batch8_prompts_128_to_2048_capacity_6144(pair):
     engine, model, oracle = pair
     rng = np.random.default_rng(2005)
     B, cap = 8, 6144
@@ -249,6 +249,6 @@ def test_cfg5_batch8_prompts_128_to_2048_capacity_6144(pair):
     gpu = s.step(toks)
     s.close()
     for b in range(B):
-        print(f"[cfg5] sequence {b}: KV {pos[b] + 1}", flush=True)
+        print(f"[batch8] sequence {b}: KV {pos[b] + 1}", flush=True)
         ref = oracle_step_from(model, oracle, kv[b], pos[b], toks[b], cap)
         check_fidelity(gpu[b], ref[0], ref[1])

@@ -6,7 +6,7 @@ MUSIC_END row (local 0) plus the codec rows [CODEC_OFFSET, CODEC_OFFSET +
 CODEC_SIZE). Model: one layer of the 3B shape (hidden 3072, 24/8 heads, FFN
 8192) with the YuE2 vocabulary (184704 rows), N(0, 0.02) weights. After a
 prefill and after one decode step, every phase's logits are compared with
-oracle.project(h, phase) under the north-star logit tolerance (2e-2 abs +
+oracle.project(h, phase) under the logit tolerance (2e-2 abs +
 1e-2 rel: one layer, where it holds), and the abc / semantic slices must be
 bit-identical to the same rows of the GPU's own full projection.
 """

@@ -66,8 +66,8 @@ CASES = [
     # name, sampling overrides, branches/cfg, phase, logits kind
     ("greedy", dict(temperature=0, top_k=1, top_p=1), 1, 1.0, "full", "normal"),
     ("greedy-ties", dict(temperature=0, top_k=1, top_p=1), 1, 1.0, "full", "ties"),
-    ("cfg3", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "normal"),
-    ("cfg3-ties", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "ties"),
+    ("cfg-pair", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "normal"),
+    ("cfg-pair-ties", dict(temperature=1.0, top_k=50, top_p=0.93), 2, 1.5, "full", "ties"),
     ("topk-only", dict(temperature=0.7, top_k=20, top_p=1.0), 1, 1.0, "full", "normal"),
     ("topp-flat", dict(temperature=1.0, top_k=5000, top_p=0.5), 1, 1.0, "full", "flat"),
     ("all-vocab", dict(temperature=1.3, top_k=100000, top_p=1.0), 1, 1.0, "full", "normal"),
