@@ -1,7 +1,9 @@
 // Split-K flash-decode attention for one layer on gfx950 (head_dim 128),
 // one kernel per layer: a one-dimensional grid of max_splits * batch * Hkv
-// workgroups of 256 threads, block = split * (batch * Hkv) + bh (the splits
-// of one (branch, kv head) spread over the XCDs). The workgroup body is
+// workgroups of 256 threads, block = split * (batch * Hkv) + bh (with
+// batch * Hkv a multiple of 8, round-robin dispatch puts the splits of one
+// (branch, kv head) on one XCD; the partial hand-off does not rely on it and
+// uses device-scope stores and loads). The workgroup body is
 // attn_block.h. The chunk length is derived on device from pos[b], so one
 // captured graph serves every KV length up to capacity.
 #include <cmath>
