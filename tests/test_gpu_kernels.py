@@ -113,6 +113,7 @@ def prep_qk(oracle, raw, gain, pos, theta=5e5):
     (24, 8, [4095], 1), (24, 8, [777], 7), (16, 8, [300], 32), (4, 2, [50], 8),
     (24, 8, [513, 1535], 32), (24, 8, [100, 1200, 7, 2047, 64, 500, 9, 1000], 32),
     (24, 8, [8191], 64),  # KV 8192: one launch of the long-context decode
+    (24, 8, [24575], 64),  # the last position of the 24576-token context
     # every other accepted heads-per-kv-head ratio: G = 1 (one head per wave
     # in the prologue), 4, 6 and 8 (two and three heads per wave)
     (8, 8, [15], 64), (8, 8, [300, 4095], 32),
@@ -357,7 +358,10 @@ def test_op_scratch_is_per_stream(torch, yuear_lib):
                                                    (2100, 40, 24, 8),
                                                    # the 3000-token prefill, one pass and
                                                    # its last chunk after 2048 cached keys
-                                                   (3000, 0, 24, 8), (952, 2048, 24, 8)])
+                                                   (3000, 0, 24, 8), (952, 2048, 24, 8),
+                                                   # the last 100 queries of the 24576-token
+                                                   # context
+                                                   (100, 24476, 24, 8)])
 def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, heads, kv_heads):
     rng = np.random.default_rng(T + pos0)
     cap = yuear_lib.kv_slots(pos0 + T + 3)
