@@ -139,6 +139,39 @@ def test_lifecycle_and_capacity_errors(tiny):
         s.step(1)
 
 
+def test_full_context_last_step_matches_oracle(yuear_lib, oracle):
+    # a session of the whole 24576-token context (the capacity range of
+    # ar.cpp:98-132): prefill to 24570, graph steps to the last slot 24575,
+    # that step against the oracle decoding from the GPU's cache (RoPE's last
+    # table row, every cache block), then the budget error with nothing moved
+    cfg = dict(TINY, max_position_embeddings=24576)
+    w = yuear_lib.random_weights(cfg, 11, 0.02, 0.1)
+    engine, model = yuear_lib.Engine(cfg, w), oracle.Model(cfg, w)
+    rng = np.random.default_rng(24576)
+    n0, last = 24570, 24575
+    s = engine.session(1, 24576)
+    s.prefill(0, rng.integers(0, cfg["vocab_size"], n0).tolist())
+    toks = [int(t) for t in rng.integers(0, cfg["vocab_size"], last - n0 + 1)]
+    for t in toks[:-1]:
+        s.step(t)
+    assert s.position(0) == last
+    kv = [s.read_kv(layer, 0, last) for layer in range(cfg["num_hidden_layers"])]
+    got = s.step(toks[-1])[0]
+    cache = model.cache(24576)
+    for layer, (k, v) in enumerate(kv):
+        cache.keys(layer)[:, :last] = k
+        cache.values(layer)[:, :last] = v
+    cache.offset = last
+    want = model.step(toks[-1], cache)
+    assert within(got, want).all()
+    assert s.position(0) == 24576
+    with pytest.raises(ValueError, match="budget"):
+        s.step(1)
+    assert s.position(0) == 24576
+    s.close()
+    engine.close()
+
+
 def test_generate_tokens_greedy_matches_oracle_teacher_forced(tiny, oracle):
     engine, model, _ = tiny
     prefix = [3, 17, 255, 1, 98]
