@@ -62,6 +62,25 @@ def test_tiny_prefill_and_steps_match_oracle_and_golden(tiny):
     assert s.position(0) == len(g["prefix"]) + len(g["steps"])
 
 
+def test_model_without_qk_norm_matches_oracle(yuear_lib, oracle):
+    # q/k RMSNorm off (no gains): the prefill's q/k preparation and the decode
+    # attention's prologue apply RoPE only
+    cfg = dict(TINY, qk_norm=False)
+    w = yuear_lib.random_weights(cfg, 5, 0.02, 0.1)
+    engine, model = yuear_lib.Engine(cfg, w), oracle.Model(cfg, w)
+    rng = np.random.default_rng(5)
+    prefix = rng.integers(0, cfg["vocab_size"], 37).tolist()
+    s = engine.session(1, 48)
+    cache = model.cache(48)
+    got, want = [s.prefill(0, prefix)], [model.prefill(prefix, cache)]
+    for t in rng.integers(0, cfg["vocab_size"], 5):
+        got.append(s.step(int(t))[0])
+        want.append(model.step(int(t), cache))
+    s.close()
+    engine.close()
+    assert within(np.stack(got), np.stack(want)).all()
+
+
 def test_chunked_prefill_is_bit_identical_to_one_pass(tiny):
     engine, _, _ = tiny
     ids = [5, 9, 14, 200, 33, 1, 511, 256, 3]

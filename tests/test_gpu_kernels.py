@@ -165,6 +165,32 @@ def test_attention_decode_matches_oracle(torch, yuear_lib, oracle, heads, kv_hea
         np.testing.assert_array_equal(gv[b][:, others], cache_v[b][:, others])
 
 
+def test_attention_decode_without_qk_norm_matches_oracle(torch, yuear_lib, oracle):
+    # a model without q/k RMSNorm (null gains): RoPE only, at the last row of
+    # a RoPE table sized to the position (ar.cpp:268-277 with the norms off)
+    rng = np.random.default_rng(77)
+    heads, kv_heads, pos = 24, 8, 1000
+    cap = yuear_lib.kv_slots(pos + 1)
+    qkv = bf(rng.normal(size=(1, (heads + 2 * kv_heads) * 128)))
+    cache_k = bf(rng.normal(size=(1, kv_heads, cap, 128)))
+    cache_v = bf(rng.normal(size=(1, kv_heads, cap, 128)))
+    cos, sin = yuear_lib.rope_table(pos + 1, 128, 5e5)
+    q = prep_qk(oracle, qkv[0, :heads * 128].reshape(heads, 128), None, pos)
+    k = prep_qk(oracle, qkv[0, heads * 128:(heads + kv_heads) * 128].reshape(kv_heads, 128),
+                None, pos)
+    K, V = cache_k[0].copy(), cache_v[0].copy()
+    K[:, pos], V[:, pos] = k, qkv[0, (heads + kv_heads) * 128:].reshape(kv_heads, 128)
+    ref = oracle.attention(q[None], K, V, pos)
+    a = [dev(torch, t) for t in (qkv, cos, sin, cache_k, yuear_lib.v_blocked(cache_v))]
+    dpos = dev(torch, np.array([pos], np.int32))
+    out = dev(torch, np.zeros((1, heads * 128), np.uint16))
+    assert yuear_lib.lib.yuear_op_attention_decode(
+        a[0].data_ptr(), None, None, 1e-5, a[1].data_ptr(), a[2].data_ptr(), a[3].data_ptr(),
+        a[4].data_ptr(), dpos.data_ptr(), heads, kv_heads, cap, 1, 32, out.data_ptr(), None) == 0
+    assert_close_bf16(host(torch, out), ref, exact_frac=0.8)
+    assert ulps_bf16(host(torch, a[3])[0][:, pos], k).max() <= 1
+
+
 def test_attention_decode_ignores_unused_slots(torch, yuear_lib):
     # vendor test_cuda_graph.py:62-79: slots beyond the position are invisible
     rng = np.random.default_rng(9)

@@ -92,7 +92,9 @@ __device__ __forceinline__ void attn_block(const AttnDecodeParams &p, float scal
       const uint16_t *gain = h < G ? p.q_norm : p.k_norm;
       has_gain[j] = gain != nullptr;
       load_rope(nr[j], cs, sn, lane);
-      load_gain(nr[j], has_gain[j] ? gain : cs, lane);
+      // without a gain the (unused) load reads the head's own 128 inputs,
+      // which are always in bounds
+      load_gain(nr[j], has_gain[j] ? gain : row + col, lane);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the prologue inputs ahead of K/V
     u32x4 kr[8], vr[8];

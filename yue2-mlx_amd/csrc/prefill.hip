@@ -98,17 +98,27 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
   if (h < p.heads + p.kv_heads) {
     const bool is_q = h < p.heads;
     const uint16_t *gain = is_q ? p.q_norm : p.k_norm;
-    NormRope r;
-    if (gain)
-      load_gain(r, gain, lane);
+    // the gains (without a gain the unused load reads this head's 128 inputs
+    // of the block's first row, always in bounds), then every row's RoPE
+    // entries (positions clamped into [lo, hi)), all issued together so no
+    // row waits for its own round trip
+    NormRope g;
+    load_gain(g, gain ? gain : p.qkv + size_t(lo - p.pos0) * p.qkv_stride + size_t(h) * 128, lane);
+    NormRope r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int pos = min(max(base + j, lo), hi - 1);
+      load_rope(r[j], p.rope_cos + size_t(pos) * 64, p.rope_sin + size_t(pos) * 64, lane);
+      r[j].g0 = g.g0;
+      r[j].g1 = g.g1;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int pos = base + j;
+      float y0, y1;
+      norm_rope_apply(bflo(v[j]), bfhi(v[j]), gain != nullptr, p.eps, r[j], lane, y0, y1);
       if (pos < lo || pos >= hi)  // uniform per wave
         continue;
-      load_rope(r, p.rope_cos + size_t(pos) * 64, p.rope_sin + size_t(pos) * 64, lane);
-      float y0, y1;
-      norm_rope_apply(bflo(v[j]), bfhi(v[j]), gain != nullptr, p.eps, r, lane, y0, y1);
       uint32_t *dst =
           is_q ? reinterpret_cast<uint32_t *>(p.q_out + (size_t(pos - p.pos0) * p.heads + h) * 128)
                : reinterpret_cast<uint32_t *>(p.k_cache +
