@@ -290,20 +290,6 @@ __device__ __forceinline__ void norm_rope_apply(float x0, float x1, bool has_gai
   }
 }
 
-// Both steps with the loads in place; cs/sn point at the bf16 cos/sin row of
-// the position. (GainPtr: a plain or an address-space-qualified pointer.)
-template <class GainPtr>
-__device__ __forceinline__ void norm_rope_head(float x0, float x1, GainPtr gain,
-                                               float eps, const uint16_t *cs,
-                                               const uint16_t *sn, int lane, float &y0,
-                                               float &y1) {
-  NormRope r;
-  load_rope(r, cs, sn, lane);
-  if (gain)
-    load_gain(r, gain, lane);
-  norm_rope_apply(x0, x1, bool(gain), eps, r, lane, y0, y1);
-}
-
 #endif
 
 }  // namespace yuear
