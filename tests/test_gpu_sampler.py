@@ -316,3 +316,41 @@ def test_sampler_known_answers_on_device(engine_yue2):
              for seed in range(50)}
     assert drawn == {1}
     session.close()
+
+
+@pytest.mark.parametrize("phase", ["full", "abc", "semantic"])
+@pytest.mark.parametrize("branches,cfg", [(1, 1.0), (2, 1.5)])
+def test_sampler_random_configurations(engine_yue2, oracle, phase, branches, cfg):
+    # seeded sweep over the sampling space (sampling.cpp:38-134, 247-250):
+    # temperature (greedy included), top k on both sides of the split form's
+    # 128, top p, repetition penalty and window over a history of the phase's
+    # native ids (rows boosted so the penalty matters), min tokens before and
+    # after the step, legacy on and off, five logit shapes; every draw
+    # identical to the oracle's
+    rng = np.random.default_rng(1000 * branches + {"full": 1, "abc": 2, "semantic": 3}[phase])
+    session = engine_yue2.session(branches, 64, phase)
+    n = session.vocab
+    to_native = oracle.lib().oracle_local_to_native
+    for trial in range(24):
+        sampling = dict(temperature=float(rng.choice([0.0, 0.6, 1.0, 1.4])),
+                        top_k=int(rng.choice([1, 7, 50, 100, 130, 400, 3000, 100000])),
+                        top_p=float(rng.choice([0.3, 0.8, 0.93, 1.0])),
+                        repetition_penalty=float(rng.choice([1.0, 1.1, 1.5])),
+                        penalty_window=int(rng.choice([5, 50, 100])),
+                        min_tokens=int(rng.choice([0, 10])), max_tokens=9000)
+        kind = str(rng.choice(["normal", "ties", "peaked", "flat", "integers"]))
+        x = logits_for(rng, kind, branches, n)
+        local = rng.integers(0, min(n, 64), size=int(rng.integers(0, 40)))
+        hist = [int(to_native(int(t), oracle.PHASES[phase])) for t in local]
+        if len(local):  # lift the history's rows to the top so the penalty decides
+            import cpu_ref
+            f = cpu_ref.bf16_to_f32(x)
+            f[:, local] += 4.0
+            x = bf(f)
+        session.write_logits(x)
+        legacy = bool(rng.integers(0, 2))
+        seed, step = int(rng.integers(0, 2**62)), int(rng.integers(0, 20))
+        got = session.sample(sampling, seed, step, history=hist, cfg_scale=cfg, legacy_off=legacy)
+        want = oracle_token(oracle, x, sampling, seed, step, hist, phase, cfg, legacy)
+        assert got == want, (trial, sampling, kind, legacy, step, got, want)
+    session.close()
