@@ -101,6 +101,48 @@ def test_gemv_matches_oracle(torch, yuear_lib, oracle, n, k, batch, norm, epilog
     assert_close_bf16(got, ref, scale=scale, exact_frac=0.9)
 
 
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 8])
+def test_gemv_random_shapes_and_strides(torch, yuear_lib, oracle, batch):
+    """Seeded sweep per batch size: random N, K (the MFMA form's hidden sizes
+    among them), RMSNorm on or off, all three epilogues, activation rows
+    padded past K and output rows padded past N; outputs against the oracle
+    and every padding element of y left as it was."""
+    rng = np.random.default_rng(777 + batch)
+    for trial in range(6):
+        k = int(rng.choice([3072, 8192, 2048, 8 * int(rng.integers(1, 1025))]))
+        epilogue, norm = int(rng.integers(0, 3)), bool(rng.integers(0, 2))
+        n = 2 * int(rng.integers(1, 1500)) if epilogue == 2 else int(rng.integers(1, 3000))
+        out_n = n // 2 if epilogue == 2 else n
+        xs, ys = k + 8 * int(rng.integers(0, 3)), out_n + int(rng.integers(0, 9))
+        w = bf(rng.normal(size=(n, k)) * 0.02)
+        x = bf(rng.normal(size=(batch, xs)))
+        g = bf(1 + rng.normal(size=k) * 0.1)
+        y0 = bf(rng.normal(size=(batch, ys)))
+        xk = np.ascontiguousarray(x[:, :k])
+        h = oracle.rms_norm(xk, g, 1e-5) if norm else xk
+        acc = oracle.linear(h, w)
+        if epilogue == 0:
+            ref = acc
+        elif epilogue == 1:
+            ref = bf(f(y0[:, :n]) + f(acc))
+        else:
+            ref = oracle.silu_mul(acc[:, 0::2], acc[:, 1::2])
+        dw, dx, dg, dy = dev(torch, w), dev(torch, x), dev(torch, g), dev(torch, y0)
+        assert yuear_lib.lib.yuear_op_gemv(dw.data_ptr(), n, k, batch, dx.data_ptr(), xs,
+                                           dg.data_ptr() if norm else None, 1e-5, dy.data_ptr(),
+                                           ys, epilogue, None) == 0
+        got = host(torch, dy)
+        case = (trial, n, k, xs, ys, norm, epilogue)
+        np.testing.assert_array_equal(got[:, out_n:], y0[:, out_n:], err_msg=str(case))
+        scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+        assert_close_bf16(got[:, :out_n], ref, scale=scale, exact_frac=0.9)
+        # overlapping rows and an empty K are refused before any launch
+        for bad_xs, bad_ys, bad_k in ((k - 8, ys, k), (xs, out_n - 1, k), (xs, ys, 0)):
+            assert yuear_lib.lib.yuear_op_gemv(dw.data_ptr(), n, bad_k, batch, dx.data_ptr(),
+                                               bad_xs, dg.data_ptr() if norm else None, 1e-5,
+                                               dy.data_ptr(), bad_ys, epilogue, None) == 1, case
+
+
 def prep_qk(oracle, raw, gain, pos, theta=5e5):
     """q/k RMSNorm over each head, then RoPE at `pos` (ar.cpp:268-277)."""
     x = oracle.rms_norm(raw, gain, 1e-5) if gain is not None else raw
@@ -303,6 +345,39 @@ def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residua
     assert_close_bf16(host(torch, dc), ref, scale=scale, exact_frac=0.9)
     assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), k, dw.data_ptr(), m, n, k,
                                             dc.data_ptr(), n, residual, 6, None) == 1
+
+
+@pytest.mark.parametrize("shape", range(6))
+def test_gemm_random_shapes_and_strides(torch, yuear_lib, oracle, shape):
+    """Seeded sweep per tile shape: ragged M, N and K, A rows padded past K
+    (lda > k, the padding filled with other values), C rows padded past the
+    output (ldc > n, odd strides included) and all three epilogues; outputs
+    against the oracle, and every padding element of C left as it was."""
+    rng = np.random.default_rng(4242 + shape)
+    for trial in range(5):
+        m, k = int(rng.integers(1, 600)), 64 * int(rng.integers(1, 13))
+        residual = int(rng.integers(0, 3))
+        n = 2 * int(rng.integers(1, 450)) if residual == 2 else int(rng.integers(1, 900))
+        out_n = n // 2 if residual == 2 else n
+        lda, ldc = k + 8 * int(rng.integers(0, 3)), out_n + int(rng.integers(0, 6))
+        a = bf(rng.normal(size=(m, lda)))
+        w = bf(rng.normal(size=(n, k)) * 0.05)
+        c0 = bf(rng.normal(size=(m, ldc)) * (1.0 if residual == 1 else 7.0))
+        da, dw, dc = dev(torch, a), dev(torch, w), dev(torch, c0)
+        assert yuear_lib.lib.yuear_op_gemm_tile(da.data_ptr(), lda, dw.data_ptr(), m, n, k,
+                                                dc.data_ptr(), ldc, residual, shape, None) == 0
+        got = host(torch, dc)
+        acc = oracle.linear(np.ascontiguousarray(a[:, :k]), w)
+        if residual == 2:
+            ref = oracle.silu_mul(acc[:, 0::2], acc[:, 1::2])
+        elif residual == 1:
+            ref = bf(f(c0[:, :n]) + f(acc))
+        else:
+            ref = acc
+        case = (trial, m, n, k, lda, ldc, residual)
+        np.testing.assert_array_equal(got[:, out_n:], c0[:, out_n:], err_msg=str(case))
+        scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max()) if residual != 2 else None
+        assert_close_bf16(got[:, :out_n], ref, scale=scale, exact_frac=0.9)
 
 
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])

@@ -115,6 +115,11 @@ def test_qgemv_rejects_unsupported_shapes(torch, yuear_lib):
         rc = yuear_lib.lib.yuear_op_qgemv(d.data_ptr(), d.data_ptr(), bits, 8, k, batch,
                                           y.data_ptr(), k, None, 1e-5, y.data_ptr(), 8, 0, None)
         assert rc != 0, (bits, k, batch)
+    # rows that would overlap: activation stride below k, output stride below n
+    for xs, ys in ((256 - 8, 8), (256, 7)):
+        rc = yuear_lib.lib.yuear_op_qgemv(d.data_ptr(), d.data_ptr(), 4, 8, 256, 2,
+                                          y.data_ptr(), xs, None, 1e-5, y.data_ptr(), ys, 0, None)
+        assert rc != 0, (xs, ys)
 
 
 @pytest.mark.parametrize("bits", [4, 8])

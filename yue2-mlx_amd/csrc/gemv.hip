@@ -61,8 +61,12 @@ hipError_t launch_b(const GemvParams &p, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_gemv(const GemvParams &p, hipStream_t s) {
-  if (p.k % 8 || p.k > 8192 || p.n < 1 || p.batch < 1 || p.batch > 8 ||
-      (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2))
+  // rows must not overlap: activation rows (read, or written as the gather's
+  // copy-out) at least k apart, output rows at least the output width apart
+  const int out_n = p.epilogue == kEpiSwiGLU ? p.n / 2 : p.n;
+  if (p.k < 8 || p.k % 8 || p.k > 8192 || p.n < 1 || p.batch < 1 || p.batch > 8 ||
+      (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2) ||
+      ((!p.embed || p.x_out) && p.x_stride < p.k) || p.y_stride < out_n)
     return hipErrorInvalidValue;
   if (p.bits && p.batch <= 2)  // quantized weights (qgemv.hip)
     return launch_qgemv(p, s);

@@ -419,8 +419,10 @@ bool qgemv_supported(int bits, int k, int batch) {
 
 hipError_t launch_qgemv(const GemvParams &p, hipStream_t s) {
   Shape sh;
+  const int out_n = p.epilogue == kEpiSwiGLU ? p.n / 2 : p.n;  // rows must not overlap
   if (!qgemv_shape(p.bits, p.k, sh) || p.batch < 1 || p.batch > 2 || p.n < 1 || !p.qw ||
-      !p.qsb || (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2))
+      !p.qsb || (p.x_stride % 8 && !p.embed) || (p.epilogue == kEpiSwiGLU && p.n % 2) ||
+      ((!p.embed || p.x_out) && p.x_stride < p.k) || p.y_stride < out_n)
     return hipErrorInvalidValue;
   if (p.bits == 4)
     return p.batch == 1 ? launch_bb<1, 4>(p, sh, s) : launch_bb<2, 4>(p, sh, s);
