@@ -251,7 +251,9 @@ int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,
  * qkv [batch][(Hq+2Hkv)*128], caches [batch][Hkv] x cap slots (cap a
  * multiple of 32; K row-major [cap][128], V in 32-slot blocks stored
  * dim-major, element (t, d) at (t/32)*4096 + d*32 + t%32), pos [batch],
- * rope tables [positions][64], out [batch][Hq*128]. */
+ * rope tables [positions][64] with a row for every position a branch is
+ * at (pos < capacity; a branch whose pos is outside [0, capacity) is left
+ * untouched), out [batch][Hq*128]; null q/k norm gains skip the RMSNorm. */
 int32_t yuear_op_attention_decode(
     const uint16_t *dev_qkv, const uint16_t *dev_q_norm,
     const uint16_t *dev_k_norm, float eps, const uint16_t *dev_rope_cos,

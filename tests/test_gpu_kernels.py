@@ -476,3 +476,9 @@ def test_attention_prefill_matches_oracle(torch, yuear_lib, oracle, T, pos0, hea
                                                     a[2].data_ptr(), T, pos0, heads, kv_heads,
                                                     cap, out.data_ptr(), None) == 0
     assert_close_bf16(host(torch, out), ref, exact_frac=0.8)
+    # a negative start, a range past the capacity and a head count below the
+    # kv heads are refused before any launch
+    for t_, p0, hq in ((T, -1, heads), (T, cap - T + 1, heads), (T, pos0, 0)):
+        assert yuear_lib.lib.yuear_op_attention_prefill(
+            a[0].data_ptr(), a[1].data_ptr(), a[2].data_ptr(), t_, p0, hq, kv_heads, cap,
+            out.data_ptr(), None) == 1, (t_, p0, hq)

@@ -221,8 +221,9 @@ hipError_t launch_qk_prep(const QkPrepParams &p, hipStream_t s) {
 }
 
 hipError_t launch_attn_prefill(const AttnPrefillParams &p, hipStream_t s) {
-  if (p.head_dim != 128 || p.tokens < 1 || p.kv_heads < 1 || p.heads % p.kv_heads ||
-      p.pos0 + p.tokens > p.capacity || p.capacity % attn::kBlock)
+  if (p.head_dim != 128 || p.tokens < 1 || p.kv_heads < 1 || p.heads < p.kv_heads ||
+      p.heads % p.kv_heads || p.pos0 < 0 || p.pos0 + p.tokens > p.capacity ||
+      p.capacity % attn::kBlock)
     return hipErrorInvalidValue;
   const float qscale = float(std::pow(128.0, -0.5)) * 1.4426950408889634f;
   if (p.heads * ((p.tokens + 63) / 64) >= attn::kTile64MinGroups)
