@@ -81,6 +81,65 @@ def test_model_without_qk_norm_matches_oracle(yuear_lib, oracle):
     assert within(np.stack(got), np.stack(want)).all()
 
 
+# (hidden, intermediate, layers, heads, kv heads, vocab, qk_norm, branches):
+# widths that are and are not the batched MFMA form's (2048 / 3072 / 6144 /
+# 8192), every accepted heads-per-kv-head ratio, one to five branches
+RANDOM_MODELS = [
+    (64, 128, 1, 1, 1, 300, True, 1),
+    (320, 704, 2, 6, 1, 1000, False, 2),
+    (1024, 1536, 3, 8, 2, 4099, True, 3),
+    (2048, 6144, 1, 16, 8, 2048, True, 5),
+    (576, 2048, 2, 24, 8, 777, False, 4),
+    (1536, 512, 1, 32, 4, 3000, True, 2),
+]
+
+
+@pytest.mark.parametrize("model", RANDOM_MODELS, ids=[f"h{m[0]}-f{m[1]}-l{m[2]}-{m[3]}x{m[4]}-b{m[7]}"
+                                                      for m in RANDOM_MODELS])
+def test_random_model_shapes_match_oracle(yuear_lib, oracle, model):
+    # the engine across model shapes (ar.cpp:133-245 configs): per-branch
+    # prefills of random lengths, then batched steps. Every prefill, and
+    # every step recomputed by the oracle from the GPU's own cache, within
+    # the per-logit bound; the oracle decoding from its own cache drifts by
+    # the caches' bf16 rounding differences (a few units of the logits' last
+    # place on a handful of logits), so against it nearly every logit is
+    # within the bound and none further than 4 bf16 units of the scale
+    H, F, layers, hq, hkv, vocab, qk_norm, branches = model
+    cfg = dict(hidden_size=H, intermediate_size=F, num_hidden_layers=layers,
+               num_attention_heads=hq, num_key_value_heads=hkv, head_dim=128, vocab_size=vocab,
+               max_position_embeddings=512, rms_norm_eps=1e-5, rope_theta=5e5, qk_norm=qk_norm)
+    rng = np.random.default_rng(H + F + hq)
+    w = yuear_lib.random_weights(cfg, int(rng.integers(0, 1000)), 0.02, 0.1)
+    engine, ref = yuear_lib.Engine(cfg, w), oracle.Model(cfg, w)
+    cap = 320
+    s = engine.session(branches, cap)
+    caches = [ref.cache(cap) for _ in range(branches)]
+    lens = []
+    for b in range(branches):
+        prefix = rng.integers(0, vocab, int(rng.integers(1, 300))).tolist()
+        lens.append(len(prefix))
+        got, want = s.prefill(b, prefix), ref.prefill(prefix, caches[b])
+        assert within(got, want).all(), ("prefill", b)
+    for step in range(4):
+        toks = [int(t) for t in rng.integers(0, vocab, branches)]
+        kv = [[s.read_kv(layer, b, lens[b] + step) for layer in range(layers)]
+              for b in range(branches)]
+        got = s.step(toks)
+        for b in range(branches):
+            mine = ref.cache(cap)
+            for layer, (k, v) in enumerate(kv[b]):
+                mine.keys(layer)[:, :lens[b] + step] = k
+                mine.values(layer)[:, :lens[b] + step] = v
+            mine.offset = lens[b] + step
+            assert within(got[b], ref.step(toks[b], mine)).all(), ("step from GPU cache", step, b)
+            want = ref.step(toks[b], caches[b])
+            err = np.abs(f(got[b]) - f(want))
+            assert np.mean(within(got[b], want)) >= 0.99, ("step", step, b)
+            assert err.max() <= 2.0 ** -6 * np.abs(f(want)).max(), ("step", step, b, err.max())
+    s.close()
+    engine.close()
+
+
 def test_chunked_prefill_is_bit_identical_to_one_pass(tiny):
     engine, _, _ = tiny
     ids = [5, 9, 14, 200, 33, 1, 511, 256, 3]
