@@ -140,6 +140,34 @@ def test_random_model_shapes_match_oracle(yuear_lib, oracle, model):
     engine.close()
 
 
+def test_repeated_runs_are_bit_identical(yuear_lib):
+    # every reduction has a fixed order (the attention's split merge adds the
+    # splits in split order whichever workgroup arrives last, the GEMV
+    # butterflies and the GEMM's K loop are fixed): two sessions fed the same
+    # prompts and tokens give the same bits, prefill and every decode step,
+    # at one branch, the CFG pair and five branches (the MFMA form), with the
+    # 3B layer shape and ~17 attention splits per kv head
+    cfg = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=2,
+               num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=4096,
+               max_position_embeddings=4096, rms_norm_eps=1e-5, rope_theta=5e5, qk_norm=True)
+    engine = yuear_lib.Engine(cfg, seed=7)
+    rng = np.random.default_rng(7)
+    for branches in (1, 2, 5):
+        prompts = [rng.integers(0, 4096, int(rng.integers(500, 2000))).tolist()
+                   for _ in range(branches)]
+        toks = rng.integers(0, 4096, size=(12, branches))
+        runs = []
+        for _ in range(2):
+            s = engine.session(branches, 2100)
+            out = [s.prefill(b, p) for b, p in enumerate(prompts)]
+            out += [s.step([int(t) for t in row]) for row in toks]
+            runs.append(out)
+            s.close()
+        for i, (a, b) in enumerate(zip(*runs)):
+            np.testing.assert_array_equal(a, b, err_msg=f"branches {branches}, output {i}")
+    engine.close()
+
+
 def test_chunked_prefill_is_bit_identical_to_one_pass(tiny):
     engine, _, _ = tiny
     ids = [5, 9, 14, 200, 33, 1, 511, 256, 3]
