@@ -207,13 +207,12 @@ __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale
 // to 768 of 32; 768 of 64 tie, 1128 and 1536 of 64 win).
 constexpr int kTile64MinGroups = 768;
 
-#ifndef YUEAR_TILE64_STAGES
-#define YUEAR_TILE64_STAGES 2
-#endif
-// LDS ring depth (prefetch distance + 1). Two stages (32 KiB, 112 VGPRs, four
-// waves per SIMD) measured 2-4% faster than three (48 KiB, 131 VGPRs, three).
-constexpr int kTile64Stages = YUEAR_TILE64_STAGES;
-constexpr int kTile64Waves = kTile64Stages == 3 ? 3 : 4;  // waves per SIMD (LDS, registers)
+// LDS ring of two stages (32 KiB: one block ahead), filled by direct-to-LDS
+// loads, so the next block needs no registers: 96 VGPRs, five waves per SIMD
+// and five workgroups per CU (160 KiB of LDS). Three stages with register
+// staging (48 KiB, 131 VGPRs, three waves) measured 2-4% slower than two.
+constexpr int kTile64Stages = 2;
+constexpr int kTile64Waves = 5;  // waves per SIMD (LDS, registers)
 
 struct Tile64Lds {
   u32x4 k[kTile64Stages][8][64];  // [stage][piece][lane]
@@ -236,22 +235,29 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
       qb[s] = src[4 * s + r];
   }
   const int kmax = t.causal_pos >= 0 ? t.causal_pos + 16 * wave + i : t.kv_len - 1;
-  // this wave's quarter of the block at kb: K pieces 2 w, 2 w + 1 (T = w / 2,
-  // s = 2 (w % 2) + {0, 1}) and V dim tiles 2 w, 2 w + 1, for target lane
-  auto fetch = [&](int kb, u32x4(&st)[4]) {
+  // this wave's quarter of the block at kb into `stage`: K pieces 2 w, 2 w + 1
+  // (T = w / 2, s = 2 (w % 2) + {0, 1}) and V dim tiles 2 w, 2 w + 1, each a
+  // direct-to-LDS buffer load that puts lane l's 16 bytes in slot l of the
+  // piece row (the MFMA operand layout; no registers in between). Keys and
+  // blocks are clamped to the last visible one, inside both ranges.
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4 *>(t.kc), 0,
+                                                    uint32_t(t.kend) * (D * 2), 0x00020000);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4 *>(t.vc), 0, uint32_t((last >> 5) + 1) * (kBlock * D * 2), 0x00020000);
+  auto fetch = [&](int kb, int stage) {
     const int key = min(kb + key_ofs(wave >> 1, i), last);
-    const int s0 = 2 * (wave & 1);
-    st[0] = t.kc[size_t(key) * (D / 8) + 4 * s0 + r];
-    st[1] = t.kc[size_t(key) * (D / 8) + 4 * (s0 + 1) + r];
-    const u32x4 *base = t.vc + size_t(min(kb >> 5, last >> 5)) * (kBlock * D / 8);
-    st[2] = base[(32 * wave + i) * (kBlock / 8) + r];
-    st[3] = base[(32 * wave + 16 + i) * (kBlock / 8) + r];
-  };
-  auto stash = [&](int stage, const u32x4(&st)[4]) {
-    sh.k[stage][2 * wave][lane] = st[0];
-    sh.k[stage][2 * wave + 1][lane] = st[1];
-    sh.v[stage][2 * wave][lane] = st[2];
-    sh.v[stage][2 * wave + 1][lane] = st[3];
+    const uint32_t ko = uint32_t(key * (D / 8) + 8 * (wave & 1) + r) * 16;
+    const uint32_t vo = uint32_t(min(kb >> 5, last >> 5)) * (kBlock * D * 2) +
+                        uint32_t((32 * wave + i) * (kBlock / 8) + r) * 16;
+    typedef __attribute__((address_space(3))) void *lds_ptr_t;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&sh.k[stage][2 * wave][0], 16, ko, 0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&sh.k[stage][2 * wave + 1][0], 16,
+                                             ko + 64, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&sh.v[stage][2 * wave][0], 16, vo, 0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)&sh.v[stage][2 * wave + 1][0], 16,
+                                             vo + 16 * kBlock * 2, 0, 0, 0);
   };
 
   float m_run = -__builtin_inff(), l_run = 0.f;
@@ -260,21 +266,15 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
   for (int dt = 0; dt < 8; ++dt)
     o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   constexpr int S = kTile64Stages;
-  u32x4 nxt[4], nxt2[4];
-  fetch(b_lo * kBlock, nxt);
-  stash(b_lo % S, nxt);
-  if (S == 3 && b_lo + 1 < nblk)
-    fetch((b_lo + 1) * kBlock, nxt);
+  fetch(b_lo * kBlock, b_lo % S);
+  __builtin_amdgcn_s_waitcnt(0);  // (a barrier waits for no load)
   __syncthreads();
   for (int b = b_lo; b < nblk; ++b) {
     const int stage = b % S, kb = b * kBlock;
-    if constexpr (S == 3) {
-      if (b + 2 < nblk)  // uniform
-        fetch(kb + 2 * kBlock, nxt2);
-    } else {
-      if (b + 1 < nblk)
-        fetch(kb + kBlock, nxt);
-    }
+    // block b + 1 into the stage every wave finished reading before the
+    // previous barrier; in flight during this block's products
+    if (b + 1 < nblk)  // uniform
+      fetch(kb + kBlock, (b + 1) % S);
     u32x4 kr[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -334,14 +334,8 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
       for (int k = 0; k < 3; ++k)
         o[dt] = mfma(vr[dt], u32x4{pw[k][0], pw[k][1], pw[k][2], pw[k][3]}, o[dt]);
     }
-    if (b + 1 < nblk)  // block b + 1 into its stage
-      stash((b + 1) % S, nxt);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of block b + 1
     __syncthreads();
-    if (S == 3 && b + 2 < nblk) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        nxt[j] = nxt2[j];
-    }
   }
   // lane (query 16 w + i, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
   const float L = sum_halves(sum_row_pairs(l_run));
