@@ -460,6 +460,9 @@ def test_op_scratch_is_per_stream(torch, yuear_lib):
                                                    # the 3000-token prefill, one pass and
                                                    # its last chunk after 2048 cached keys
                                                    (3000, 0, 24, 8), (952, 2048, 24, 8),
+                                                   # 384 workgroups, the fewest that take the
+                                                   # 64-query tile (ragged last tile after 100)
+                                                   (1024, 0, 24, 8), (1000, 100, 24, 8),
                                                    # the last 100 queries of the 24576-token
                                                    # context
                                                    (100, 24476, 24, 8)])

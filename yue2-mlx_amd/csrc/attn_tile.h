@@ -203,9 +203,13 @@ __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale
 // attn_query_tile (fp32 scores, exp2 online softmax, P as three truncated
 // bf16 pieces, fp32 sums, bf16(o / l)), with no merge across waves.
 // Workgroups of the 64-query tile below which the 32-query key-split tile
-// is faster on MI355X's 256 CUs (measured: 384 workgroups of 64 queries lose
-// to 768 of 32; 768 of 64 tie, 1128 and 1536 of 64 win).
-constexpr int kTile64MinGroups = 768;
+// is faster on MI355X's 256 CUs (measured, causal self-attention at 24/8
+// heads: 288 workgroups of 64 queries (768 tokens) lose to 576 of 32, 23.3
+// against 22.1 us; 384 (1024 tokens) win, 30.5 against 33.5 us, and the gap
+// grows with the length: 66.6 against 85 us at 1984 tokens).
+constexpr int kTile64MinGroups = 384;
+// Key splits of a non-causal launch aim at this many workgroups.
+constexpr int kSplitTargetGroups = 768;
 
 // LDS ring of two stages (32 KiB: one block ahead), filled by direct-to-LDS
 // loads, so the next block needs no registers: 96 VGPRs, five waves per SIMD

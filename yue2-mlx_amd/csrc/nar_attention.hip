@@ -160,16 +160,16 @@ hipError_t launch_v_rows(const uint16_t *vb, int kv_stride, int heads, int n, ui
 
 namespace {
 // Key splits for a non-causal launch whose 64-query workgroups do not fill
-// the GPU: enough to reach kTile64MinGroups, each split at least 8 blocks.
+// the GPU: enough to reach kSplitTargetGroups, each split at least 8 blocks.
 // The kernel gives split z the blocks [z * per, min(nb, (z + 1) * per)),
 // per = ceil(nb / splits); the count is recomputed from per so that no
 // split is left without blocks (nb 81 over 10 splits: per 9, 9 splits).
 int nar_splits(int batch, int heads, int q_len, int kv_len, int causal) {
   const long long g64 = (long long)batch * heads * ((q_len + 63) / 64);
   const int nb = (kv_len + attn::kBlock - 1) / attn::kBlock;
-  if (causal || g64 >= attn::kTile64MinGroups)
+  if (causal || g64 >= attn::kSplitTargetGroups)
     return 1;
-  const int want = int((attn::kTile64MinGroups + g64 - 1) / g64);
+  const int want = int((attn::kSplitTargetGroups + g64 - 1) / g64);
   const int s = std::max(1, std::min(want, nb / 8));
   const int per = (nb + s - 1) / s;
   return (nb + per - 1) / per;
