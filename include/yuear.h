@@ -237,10 +237,10 @@ yuear_status yuear_session_time_kernel(yuear_session *session,
 /* ---- op-level entry points (model_ops, ar.hpp:8-19), device pointers,
  * `stream` is a hipStream_t (NULL = default stream). Scratch memory (the
  * batched GEMV's staging rows, the decode attention's split partials and
- * arrival counters) is per (device, stream): calls on different streams
- * never share it. The first call on a stream (or one needing a larger
- * buffer) allocates, so make it outside graph capture; yuear_op_gemm uses
- * no scratch. ---- */
+ * arrival counters, the split-K GEMM's partials) is per (device, stream):
+ * calls on different streams never share it. The first call on a stream (or
+ * one needing a larger buffer) allocates, so make it outside graph capture;
+ * yuear_op_gemm and yuear_op_gemm_tile use no scratch. ---- */
 /* y[b][r] = bf16(x[b] . W[row(r)]) with optional RMSNorm prologue
  * (norm_w != NULL) and epilogue 0 store / 1 residual add / 2 SwiGLU pairs. */
 int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,
@@ -305,6 +305,17 @@ int32_t yuear_op_gemm(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
 int32_t yuear_op_gemm_tile(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                            int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                            int32_t ldc, int32_t residual, int32_t shape, void *stream);
+/* Test hook (no counterpart in the reference): yuear_op_gemm_tile with K
+ * split over `splits` workgroups per tile (1..16; k / 64 a multiple of
+ * splits), each summing its K range into fp32 partials (splits * m * n
+ * floats, in a per-(device, stream) buffer that the first such call on a
+ * stream allocates, so make it outside graph capture) that a second kernel
+ * adds in split order before the epilogue: the form the engine's prefill
+ * GEMMs take when their tiles alone leave most CUs idle. */
+int32_t yuear_op_gemm_split(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
+                            int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
+                            int32_t ldc, int32_t residual, int32_t shape,
+                            int32_t splits, void *stream);
 /* Causal fp32-opmath attention for T queries at positions pos0 + t over one
  * branch's caches ([Hkv] x cap slots, the layout of
  * yuear_op_attention_decode). */

@@ -380,11 +380,47 @@ def test_gemm_random_shapes_and_strides(torch, yuear_lib, oracle, shape):
         assert_close_bf16(got[:, :out_n], ref, scale=scale, exact_frac=0.9)
 
 
+@pytest.mark.parametrize("m,n,k,residual,splits", [
+    (300, 1000, 512, 0, 2), (517, 776, 1024, 1, 4), (129, 200, 3072, 2, 6),
+    (64, 3072, 8192, 1, 8), (1, 200, 1024, 0, 16)])
+def test_gemm_split_k_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual, splits):
+    """The split-K form (each split's K range summed into fp32 partials, the
+    splits added in split order before the epilogue) on every tile shape:
+    against the oracle, identical bits on a second launch, and a split count
+    that does not divide K's 64-wide steps refused."""
+    rng = np.random.default_rng(m + n + k + splits)
+    a = bf(rng.normal(size=(m, k)))
+    w = bf(rng.normal(size=(n, k)) * 0.05)
+    out_n = n // 2 if residual == 2 else n
+    c0 = bf(rng.normal(size=(m, out_n))) if residual == 1 else np.zeros((m, out_n), np.uint16)
+    acc = oracle.linear(a, w)
+    if residual == 2:
+        ref, scale = oracle.silu_mul(acc[:, 0::2], acc[:, 1::2]), None
+    else:
+        ref = bf(f(c0) + f(acc)) if residual else acc
+        scale = max(np.abs(f(acc)).max(), np.abs(f(ref)).max())
+    da, dw = dev(torch, a), dev(torch, w)
+    for shape in range(6):
+        outs = []
+        for _ in range(2):
+            dc = dev(torch, c0)
+            assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), m, n, k,
+                                                     dc.data_ptr(), out_n, residual, shape,
+                                                     splits, None) == 0
+            outs.append(host(torch, dc))
+        np.testing.assert_array_equal(outs[0], outs[1], err_msg=f"shape {shape}")
+        assert_close_bf16(outs[0], ref, scale=scale, exact_frac=0.9)
+    bad = next(z for z in range(2, 17) if (k // 64) % z)
+    assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), m, n, k,
+                                             dev(torch, c0).data_ptr(), out_n, residual, 0, bad,
+                                             None) == 1
+
+
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])
 def test_gemm_split_k_is_deterministic(torch, yuear_lib, m, n, k):
-    """Every output sums its K products in the same order on each launch
-    (no split of K across workgroups, no atomics), so repeated launches of
-    narrow, wide and deep shapes give identical bits."""
+    """Every output sums its K products in the same order on each launch (no
+    atomics; yuear_op_gemm has no workspace, so K is never split), so
+    repeated launches of narrow, wide and deep shapes give identical bits."""
     rng = np.random.default_rng(m + 3 * n)
     a = dev(torch, bf(rng.normal(size=(m, k))))
     w = dev(torch, bf(rng.normal(size=(n, k)) * 0.02))

@@ -90,6 +90,9 @@ const char *const kLayerNames[] = {"input_layernorm",  "post_attention_layernorm
                                    "mlp.gate_proj",    "mlp.up_proj",
                                    "mlp.down_proj"};
 constexpr int kNumLayerTensors = 11;
+// Split-K workspace of a session's prefill GEMMs: one round of 128 x 128
+// tiles on 256 CUs at two per CU (512 x 128 x 128 fp32) fits.
+constexpr size_t kSplitBytes = size_t(32) << 20;
 
 int32_t tensor_id(const std::string &name) {
   if (name == "model.embed_tokens.weight") return 0;
@@ -282,6 +285,7 @@ struct yuear_session {
   int chunk = 0;
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
            *pact = nullptr;
+  float *psplit = nullptr;  // split-K partials of the prefill GEMMs (kSplitBytes)
   int32_t *pids = nullptr;
   // host mirrors / pinned
   std::vector<int> host_pos;
@@ -654,8 +658,10 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.history_cap = kContext;
   S.history = S.alloc<int32_t>(size_t(S.history_cap) * sets);
   // prefill in chunks of up to 4096 tokens (~210 MB of scratch at the 3B
-  // shape): larger GEMMs fill the GPU better (M = 3000: 590 TFLOP/s against
-  // ~400 at M = 1024) and chunked equals one-pass bit for bit
+  // shape, plus the GEMMs' split-K partials): larger GEMMs fill the GPU
+  // better (M = 3000: 590 TFLOP/s against ~400 at M = 1024). A chunked
+  // prefill equals the one-pass prefill bit for bit when their GEMMs take the
+  // same tile shape and split count (shapes are chosen per M)
   S.chunk = std::min(capacity, 4096);
   const size_t T = S.chunk;
   S.px = S.alloc<uint16_t>(T * c.H);
@@ -664,6 +670,7 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
   S.pq = S.alloc<uint16_t>(T * c.Hq * c.D);
   S.pattn = S.alloc<uint16_t>(T * c.Hq * c.D);
   S.pact = S.alloc<uint16_t>(T * c.F);
+  S.psplit = S.alloc<float>(kSplitBytes / 4);
   S.pids = S.alloc<int32_t>(T);
   S.host_pos.assign(branches, 0);
   HIPC(hipHostMalloc(reinterpret_cast<void **>(&S.pin_tok), size_t(kContext + 16) * 4));
@@ -940,7 +947,7 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
     for (int l = 0; l < c.layers; ++l) {
       const LayerW &L = E.layers[l];
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.input_ln, c.eps, S.ph, st));
-      GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0};
+      GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0, S.psplit, kSplitBytes};
       HIPC(launch_gemm(g, st));
       QkPrepParams qp;
       qp.qkv = S.pqkv;
@@ -972,12 +979,14 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       ap.capacity = S.kv_stride;
       ap.out = S.pattn;
       HIPC(launch_attn_prefill(ap, st));
-      GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1};
+      GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1, S.psplit,
+                    kSplitBytes};
       HIPC(launch_gemm(og, st));
       HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
-      GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pact, c.F, 2};  // SwiGLU epilogue
+      GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pact, c.F, 2, S.psplit,
+                    kSplitBytes};  // SwiGLU epilogue
       HIPC(launch_gemm(gu, st));
-      GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1};
+      GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1, S.psplit, kSplitBytes};
       HIPC(launch_gemm(dg, st));
     }
     S.host_pos[b] += T;
@@ -1847,6 +1856,26 @@ int32_t yuear_op_gemm_tile(const uint16_t *a, int32_t lda, const uint16_t *w, in
                            int32_t shape, void *stream) {
   GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
   return int32_t(launch_gemm_tile(p, shape, static_cast<hipStream_t>(stream)));
+}
+int32_t yuear_op_gemm_split(const uint16_t *a, int32_t lda, const uint16_t *w, int32_t m,
+                            int32_t n, int32_t k, uint16_t *c, int32_t ldc, int32_t residual,
+                            int32_t shape, int32_t splits, void *stream) {
+  GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (splits > 1) {
+    if (m < 1 || n < 1 || splits > 16)
+      return int32_t(hipErrorInvalidValue);
+    static OpPool pool;
+    void *buf = nullptr;
+    bool fresh = false;
+    const size_t bytes = size_t(splits) * size_t(m) * size_t(n) * 4;
+    const hipError_t e = pool.get(st, bytes, &buf, &fresh);
+    if (e != hipSuccess)
+      return int32_t(e);
+    p.part = static_cast<float *>(buf);
+    p.part_bytes = bytes;
+  }
+  return int32_t(launch_gemm_tile(p, shape, st, splits));
 }
 
 int32_t yuear_op_attention_prefill(const uint16_t *q, const uint16_t *k_cache,

@@ -52,6 +52,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 constexpr int kBK = 64;  // K per step; one LDS row = 128 bytes
+constexpr int kMaxSplits = 16;  // split-K: at most this many K ranges per tile
 
 // The kernel's only LDS object (dynamic size: 2 stages of (BM + BN) rows).
 // With a second __shared__ variable the compiler no longer tells the
@@ -91,6 +92,49 @@ __device__ __forceinline__ void swiglu_store(const GemmParams &p, int m, int n, 
   }
 }
 
+// Epilogue of a lane's 4 consecutive features n .. n + 3 (n a multiple of 4)
+// of token row m < p.m: the 8-byte form when all four are in range and rows
+// stay 8-byte aligned, else element by element.
+__device__ __forceinline__ void epilogue4(const GemmParams &p, int m, int n, const float *v) {
+  if (p.residual == 2) {
+    swiglu_store(p, m, n, v);
+    return;
+  }
+  uint16_t *c = p.c + size_t(m) * p.ldc + n;
+  if (n + 3 < p.n && (p.ldc & 3) == 0) {
+    uint2 o;
+    if (p.residual) {
+      const uint2 old = *reinterpret_cast<const uint2 *>(c);
+      o.x = pack_bf16x2(bf2f(uint16_t(old.x)) + rbf(v[0]), bf2f(uint16_t(old.x >> 16)) + rbf(v[1]));
+      o.y = pack_bf16x2(bf2f(uint16_t(old.y)) + rbf(v[2]), bf2f(uint16_t(old.y >> 16)) + rbf(v[3]));
+    } else {
+      o.x = pack_bf16x2(v[0], v[1]);
+      o.y = pack_bf16x2(v[2], v[3]);
+    }
+    *reinterpret_cast<uint2 *>(c) = o;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < p.n)
+        c[e] = p.residual ? f2bf(bf2f(c[e]) + rbf(v[e])) : f2bf(v[e]);
+  }
+}
+
+// Split-K: split s of a workgroup's K range stores its fp32 sums of the
+// 4 features at p.part[s][m][n .. n + 3]; gemm_reduce_kernel adds the splits
+// in split order and applies the epilogue.
+__device__ __forceinline__ void partial4(const GemmParams &p, int m, int n, const float *v) {
+  float *dst = p.part + (size_t(blockIdx.y) * p.m + m) * p.n + n;
+  if (n + 3 < p.n && (p.n & 3) == 0) {
+    *reinterpret_cast<float4 *>(dst) = float4{v[0], v[1], v[2], v[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < p.n)
+        dst[e] = v[e];
+  }
+}
+
 // Tile of workgroup b. Workgroups are dispatched to the 8 XCDs round-robin
 // (b % 8), each XCD with its own L2: XCD x takes the contiguous range
 // [x T / 8, (x + 1) T / 8) of a grouped order (columns of 4 tile rows), so
@@ -111,8 +155,11 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int &tm
   tn = r / rows;
 }
 
-template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
+// SPLIT: the workgroup takes K range blockIdx.y of `splits` and stores fp32
+// partial sums (a separate instantiation, so the one-pass kernels keep their
+// compile-time K range and direct epilogue).
+template <int BM, int BN, int WM, int WN, bool SPLIT>
+__device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n, int splits) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;  // 32 x 32 MFMA tiles per wave
   constexpr int ABLK = BM / 8, BLK = (BM + BN) / 8;   // 1 KiB load blocks per stage
@@ -125,6 +172,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
   const int h = lane >> 5;
   int tm, tn;
   tile_of(int(blockIdx.x), (p.m + BM - 1) / BM, tiles_n, tm, tn);
+  // split blockIdx.y of `splits` takes K [kbeg, kbeg + k / splits)
+  const int kspan = SPLIT ? p.k / splits : p.k, kbeg = SPLIT ? int(blockIdx.y) * kspan : 0;
   const int m0 = tm * BM, n0 = tn * BN;
   const auto ra = rows_rsrc(p.a + size_t(m0) * p.lda, size_t(p.m - m0) * p.lda * 2);
   const auto rw = rows_rsrc(p.w + size_t(n0) * p.k, size_t(p.n - n0) * p.k * 2);
@@ -138,7 +187,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
     const bool is_a = q < ABLK;
     const int row = 8 * (is_a ? q : q - ABLK) + (lane >> 3);
     const int kc = (lane & 7) ^ (lane >> 4) ^ (4 * (q & 1));  // f(row), BM / 8 even
-    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8) * 2;
+    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8 + kbeg) * 2;
   }
   auto dma = [&](int st, int k0) {
     char *stage = gemm_lds + st * STAGE;
@@ -163,7 +212,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
   const int f = (lane >> 1) & 7;  // f(row): row % 16 = lane % 16
   const int a_row = (wm * (BM / WM) + (lane & 31)) * 128;
   const int w_row = BM * 128 + (wn * (BN / WN) + (lane & 31)) * 128;
-  const int steps = p.k / kBK;
+  const int steps = kspan / kBK;
   bf16x8_t af[2][TM], wf[2][TN];
   // fragments of sub-step s of the stage at `stage`, W and A tiles in the
   // order the MFMAs use them, so the first MFMA waits for two reads only
@@ -243,32 +292,12 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, int tiles_n) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn * (BN / WN) + j * 32 + 8 * q + 4 * h;
-        uint16_t *c = p.c + size_t(m) * p.ldc + n;
         const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                             acc[i][j][4 * q + 3]};
-        if (p.residual == 2) {
-          swiglu_store(p, m, n, v);
-          continue;
-        }
-        if (n + 3 < p.n && (p.ldc & 3) == 0) {
-          uint2 o;
-          if (p.residual) {
-            const uint2 old = *reinterpret_cast<const uint2 *>(c);
-            o.x = pack_bf16x2(bf2f(uint16_t(old.x)) + rbf(v[0]),
-                              bf2f(uint16_t(old.x >> 16)) + rbf(v[1]));
-            o.y = pack_bf16x2(bf2f(uint16_t(old.y)) + rbf(v[2]),
-                              bf2f(uint16_t(old.y >> 16)) + rbf(v[3]));
-          } else {
-            o.x = pack_bf16x2(v[0], v[1]);
-            o.y = pack_bf16x2(v[2], v[3]);
-          }
-          *reinterpret_cast<uint2 *>(c) = o;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < p.n)
-              c[e] = p.residual ? f2bf(bf2f(c[e]) + rbf(v[e])) : f2bf(v[e]);
-        }
+        if (SPLIT)
+          partial4(p, m, n, v);
+        else
+          epilogue4(p, m, n, v);
       }
     }
   }
@@ -281,8 +310,8 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 // step), 16 x 16 accumulators (lane l: token row l % 16, features
 // 4 (l / 16) + [0, 4)). Twice the MFMAs of half the length: measured 6-7 %
 // faster than the 32 x 32 form for 256 x 256 tiles at M = 1024-3000.
-template <int BM, int BN, int WM, int WN>
-__device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
+template <int BM, int BN, int WM, int WN, bool SPLIT>
+__device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n, int splits) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int ABLK = BM / 8, BLK = (BM + BN) / 8;
@@ -295,6 +324,8 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
   const int q4 = lane >> 4;
   int tm, tn;
   tile_of(int(blockIdx.x), (p.m + BM - 1) / BM, tiles_n, tm, tn);
+  // split blockIdx.y of `splits` takes K [kbeg, kbeg + k / splits)
+  const int kspan = SPLIT ? p.k / splits : p.k, kbeg = SPLIT ? int(blockIdx.y) * kspan : 0;
   const int m0 = tm * BM, n0 = tn * BN;
   const auto ra = rows_rsrc(p.a + size_t(m0) * p.lda, size_t(p.m - m0) * p.lda * 2);
   const auto rw = rows_rsrc(p.w + size_t(n0) * p.k, size_t(p.n - n0) * p.k * 2);
@@ -305,7 +336,7 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
     const bool is_a = q < ABLK;
     const int row = 8 * (is_a ? q : q - ABLK) + (lane >> 3);
     const int kc = (lane & 7) ^ (lane >> 4) ^ (4 * (q & 1));  // f(row), BM / 8 even
-    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8) * 2;
+    goff[i] = uint32_t(row * (is_a ? p.lda : p.k) + kc * 8 + kbeg) * 2;
   }
   auto dma = [&](int st, int k0) {
     char *stage = gemm_lds + st * STAGE;
@@ -325,7 +356,7 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
   const int f = (lane >> 1) & 7;  // f(row): row % 16 = lane % 16
   const int a_row = (wm * (BM / WM) + (lane & 15)) * 128;
   const int w_row = BM * 128 + (wn * (BN / WN) + (lane & 15)) * 128;
-  const int steps = p.k / kBK;
+  const int steps = kspan / kBK;
   bf16x8_t af[2][TM], wf[2][TN];
   auto rd = [&](const char *stage, int buf, int s) {
     const int co = ((4 * s + q4) ^ f) * 16;
@@ -387,40 +418,25 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * (BN / WN) + j * 16 + 4 * q4;
-      uint16_t *c = p.c + size_t(m) * p.ldc + n;
       const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      if (p.residual == 2) {
-        swiglu_store(p, m, n, v);
-        continue;
-      }
-      if (n + 3 < p.n && (p.ldc & 3) == 0) {
-        uint2 o;
-        if (p.residual) {
-          const uint2 old = *reinterpret_cast<const uint2 *>(c);
-          o.x = pack_bf16x2(bf2f(uint16_t(old.x)) + rbf(v[0]), bf2f(uint16_t(old.x >> 16)) + rbf(v[1]));
-          o.y = pack_bf16x2(bf2f(uint16_t(old.y)) + rbf(v[2]), bf2f(uint16_t(old.y >> 16)) + rbf(v[3]));
-        } else {
-          o.x = pack_bf16x2(v[0], v[1]);
-          o.y = pack_bf16x2(v[2], v[3]);
-        }
-        *reinterpret_cast<uint2 *>(c) = o;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < p.n)
-            c[e] = p.residual ? f2bf(bf2f(c[e]) + rbf(v[e])) : f2bf(v[e]);
-      }
+      if (SPLIT)
+        partial4(p, m, n, v);
+      else
+        epilogue4(p, m, n, v);
     }
   }
 }
 
-
 // One kernel per tile shape. The kernels are not templates: this clang emits
 // no host launch stub for these kernel bodies when the kernel itself is a
 // template instantiated from host code.
-#define YUEAR_GEMM_KERNEL(NAME, BODY, BM, BN, WM, WN)                            \
-  __global__ __launch_bounds__(WM * WN * 64) void NAME(GemmParams p, int tiles_n) { \
-    BODY<BM, BN, WM, WN>(p, tiles_n);                                            \
+#define YUEAR_GEMM_KERNEL(NAME, BODY, BM, BN, WM, WN)                                        \
+  __global__ __launch_bounds__(WM * WN * 64) void NAME(GemmParams p, int tiles_n, int splits) { \
+    BODY<BM, BN, WM, WN, false>(p, tiles_n, splits);                                         \
+  }                                                                                          \
+  __global__ __launch_bounds__(WM * WN * 64) void NAME##_split(GemmParams p, int tiles_n,     \
+                                                               int splits) {                 \
+    BODY<BM, BN, WM, WN, true>(p, tiles_n, splits);                                          \
   }
 // MFMA form per shape, as measured: 16 x 16 x 32 for all but 128 x 128
 // (256 x 192 on it 2-4% faster than on 32 x 32 x 16 once its fragment reads
@@ -447,8 +463,46 @@ constexpr TileShape kShapes[] = {
     {128, 128, 2, 34.3, 40.0, 50.8}, {192, 192, 1, 41.0, 49.0, 49.0},
 };
 
+// Split-K: the sum over the splits in split order (a fixed order: the result
+// does not depend on which split finished first), then the epilogue; one
+// thread per 4 consecutive features of a row. All of a thread's partial loads
+// are issued before the first add, so a thread waits for one memory latency
+// rather than one per split.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p, int splits) {
+  const int nq = (p.n + 3) / 4;
+  const size_t total = size_t(p.m) * nq;
+  const size_t plane = size_t(p.m) * p.n;
+  for (size_t x = size_t(blockIdx.x) * 256 + threadIdx.x; x < total; x += size_t(gridDim.x) * 256) {
+    const int m = int(x / nq), n = int(x % nq) * 4;
+    const float *src = p.part + size_t(m) * p.n + n;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (n + 3 < p.n && (p.n & 3) == 0) {
+      f32x4v t[kMaxSplits];
+#pragma unroll
+      for (int z = 0; z < kMaxSplits; ++z)
+        if (z < splits)
+          t[z] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(src + z * plane));
+#pragma unroll
+      for (int z = 0; z < kMaxSplits; ++z)
+        if (z < splits) {
+          v[0] += t[z].x;
+          v[1] += t[z].y;
+          v[2] += t[z].z;
+          v[3] += t[z].w;
+        }
+    } else {
+      for (int z = 0; z < splits; ++z)
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.n)
+            v[e] += src[z * plane + e];
+    }
+    epilogue4(p, m, n, v);
+  }
+}
+
 template <int BM, int BN, int WM, int WN>
-hipError_t launch_tile(void (*kern)(GemmParams, int), const GemmParams &p, hipStream_t s) {
+hipError_t launch_tile(void (*kern)(GemmParams, int, int), const GemmParams &p, int splits,
+                       hipStream_t s) {
   const int lds = 2 * (BM + BN) * 128;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -456,7 +510,14 @@ hipError_t launch_tile(void (*kern)(GemmParams, int), const GemmParams &p, hipSt
     return e;
   const int tiles_n = (p.n + BN - 1) / BN;
   const unsigned tiles = unsigned((p.m + BM - 1) / BM) * unsigned(tiles_n);
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(WM * WN * 64), lds, s, p, tiles_n);
+  hipLaunchKernelGGL(kern, dim3(tiles, unsigned(splits)), dim3(WM * WN * 64), lds, s, p, tiles_n,
+                     splits);
+  e = hipGetLastError();
+  if (e != hipSuccess || splits == 1)
+    return e;
+  const size_t quads = size_t(p.m) * ((p.n + 3) / 4);
+  const unsigned blocks = unsigned(std::min<size_t>((quads + 255) / 256, 4096));
+  hipLaunchKernelGGL(gemm_reduce_kernel, dim3(blocks), dim3(256), 0, s, p, splits);
   return hipGetLastError();
 }
 
@@ -493,24 +554,51 @@ int gemm_tile_choice(int m, int n, int cus) {
   return best;
 }
 
-hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s) {
+int gemm_split_choice(int m, int n, int k, int shape, int cus, size_t part_bytes) {
+  if (shape < 0 || shape >= int(sizeof(kShapes) / sizeof(kShapes[0])) || m < 1 || n < 1)
+    return 1;
+  const TileShape &t = kShapes[shape];
+  const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+  const long long slots = (long long)cus * t.per_cu;
+  // only grids that leave most of the GPU idle: K is then the serial chain
+  if (tiles * 4 > slots)
+    return 1;
+  int best = 1;
+  for (int z = 2; z <= kMaxSplits; ++z) {
+    // whole 64-wide steps, at least 8 of them per split, the partials in the
+    // workspace, no more workgroups than one round
+    if ((k / kBK) % z || k / z < 8 * kBK || tiles * z > slots ||
+        size_t(z) * size_t(m) * size_t(n) * 4 > part_bytes)
+      continue;
+    best = z;
+  }
+  return best;
+}
+
+hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int splits) {
   if (p.m < 1 || p.n < 1 || p.k < kBK || p.k % kBK || p.lda < p.k || p.lda % 8 || !p.a ||
       !p.w || !p.c || p.residual < 0 || p.residual > 2 || (p.residual == 2 && p.n % 2) ||
-      p.ldc < (p.residual == 2 ? p.n / 2 : p.n))
+      p.ldc < (p.residual == 2 ? p.n / 2 : p.n) || splits < 1 || splits > kMaxSplits ||
+      (p.k / kBK) % splits ||
+      (splits > 1 && (!p.part || size_t(splits) * size_t(p.m) * size_t(p.n) * 4 > p.part_bytes)))
     return hipErrorInvalidValue;
+  const bool sp = splits > 1;
   switch (shape) {
-  case 0: return launch_tile<256, 256, 2, 4>(gemm_256x256, p, s);
-  case 1: return launch_tile<256, 128, 4, 2>(gemm_256x128, p, s);
-  case 2: return launch_tile<128, 256, 2, 4>(gemm_128x256, p, s);
-  case 3: return launch_tile<256, 192, 4, 2>(gemm_256x192, p, s);
-  case 4: return launch_tile<128, 128, 2, 2>(gemm_128x128, p, s);
-  case 5: return launch_tile<192, 192, 2, 4>(gemm_192x192, p, s);
+  case 0: return launch_tile<256, 256, 2, 4>(sp ? gemm_256x256_split : gemm_256x256, p, splits, s);
+  case 1: return launch_tile<256, 128, 4, 2>(sp ? gemm_256x128_split : gemm_256x128, p, splits, s);
+  case 2: return launch_tile<128, 256, 2, 4>(sp ? gemm_128x256_split : gemm_128x256, p, splits, s);
+  case 3: return launch_tile<256, 192, 4, 2>(sp ? gemm_256x192_split : gemm_256x192, p, splits, s);
+  case 4: return launch_tile<128, 128, 2, 2>(sp ? gemm_128x128_split : gemm_128x128, p, splits, s);
+  case 5: return launch_tile<192, 192, 2, 4>(sp ? gemm_192x192_split : gemm_192x192, p, splits, s);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
-  return launch_gemm_tile(p, gemm_tile_choice(p.m, p.n, device_cus()), s);
+  const int cus = device_cus();
+  const int shape = gemm_tile_choice(p.m, p.n, cus);
+  const int splits = p.part ? gemm_split_choice(p.m, p.n, p.k, shape, cus, p.part_bytes) : 1;
+  return launch_gemm_tile(p, shape, s, splits);
 }
 
 }  // namespace yuear
