@@ -91,8 +91,12 @@ def check_fidelity(gpu, oracle32, oracle64):
     """The reference's fidelity rule for multi-layer bf16 models
     (tools/limits.py:21-79, tools/fidelity.py:124-148): the GPU's distance to
     the fp64-accumulation oracle stays within twice the distance of the
-    fp32-accumulation oracle to it (max_abs, rms, 1 - cosine), and the argmax
-    agrees unless the top two are closer than that radius."""
+    fp32-accumulation oracle to it in max_abs and rms -- the two metrics the
+    reference derives limits for (limits.py:50-53, "RMS and maximum absolute
+    error satisfy the triangle inequality"); cosine is reported, not bounded,
+    as there: 1 - cosine grows with the square of the error, so twice the
+    radius on it would be a sqrt(2) bound on rms -- and the argmax agrees
+    unless the top two are closer than that radius."""
     radius = fidelity_metrics(oracle32, oracle64)
     got = fidelity_metrics(gpu, oracle64)
     # the per-logit bound of the single-layer tests (2e-2 abs + 1e-2 rel),
@@ -107,7 +111,6 @@ def check_fidelity(gpu, oracle32, oracle64):
     assert within["gpu"] >= 0.7 * within["oracle32"], within
     assert got["max_abs"] <= 2 * radius["max_abs"]
     assert got["rms"] <= 2 * radius["rms"]
-    assert 1 - got["cos"] <= 2 * (1 - radius["cos"])
     top = np.sort(_f64(oracle64))[-2:]
     assert _f64(gpu).argmax() == _f64(oracle64).argmax() or top[1] - top[0] < 2 * radius["max_abs"]
 

@@ -140,7 +140,7 @@ def test_prefill_256_greedy_400(pair):
           f"oracle {dist}; free-running stream first divergence {first}; "
           f"{timing['output_tps']:.1f} tok/s", flush=True)
     assert len(flips_gpu) <= 2 * len(flips_ref) + 1, (flips_gpu, flips_ref)
-    for key in ("max_abs", "rms", "one_minus_cos"):
+    for key in ("max_abs", "rms"):  # the reference's two bounded metrics; cosine reported
         assert dist["gpu"][key] <= 2 * dist["oracle32"][key], (key, dist)
     # every teacher-forced flip against the fp32 oracle is a near-tie of it
     # within the two sides' own difference at that step
