@@ -198,11 +198,12 @@ def run_long(args, engine, c):
 
 
 def run_prefill(args, engine, c):
-    """Profiling mode: `--prefills` 3000-token prefills of the 3B model (the
-    prefill half of the long-context workload), timed one by one."""
+    """Profiling mode: `--prefills` prefills of `--prefill-tokens` (3000: the
+    prefill half of the long-context workload) tokens on the 3B model, timed
+    one by one."""
     import numpy as np
     import torch
-    T = 3000
+    T = args.prefill_tokens
     rng = np.random.default_rng(args.seed + 4)
     times = []
     for i in range(args.prefills + 1):  # the first call loads code objects
@@ -218,9 +219,9 @@ def run_prefill(args, engine, c):
         log(f"[bench] prefill {i}: {(time.perf_counter() - t) * 1e3:.2f} ms")
     flops = prefill_flops(c, T)
     best = min(times)
-    return {"metric": "prefill TFLOP/s (3000 tokens)", "value": round(flops / best / 1e12, 2),
+    return {"metric": f"prefill TFLOP/s ({T} tokens)", "value": round(flops / best / 1e12, 2),
             "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
-            "data": "synthetic", "config": {"workload": "3B decoder, 3000-token prefill"},
+            "data": "synthetic", "config": {"workload": f"3B decoder, {T}-token prefill"},
             "prefill_ms": [round(t * 1e3, 3) for t in times], "prefill_flops": flops,
             "mfma_frac": round(flops / best / PEAK_BF16, 4)}
 
@@ -336,7 +337,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-launches", type=int, default=112)
     ap.add_argument("--prefills", type=int, default=3,
-                    help="--config prefill: number of timed 3000-token prefills")
+                    help="--config prefill: number of timed prefills")
+    ap.add_argument("--prefill-tokens", type=int, default=3000,
+                    help="--config prefill: prompt length of each prefill")
     ap.add_argument("--config", choices=("decode", "cfg", "long", "batch8", "nar", "prefill"),
                     default="decode",
                     help="workload (decode: the headline batch-1 KV-4096 line)")
@@ -350,6 +353,8 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path; the decode "
               "step of one sequence runs on a single GPU", file=sys.stderr)
         sys.exit(2)
+    if not 1 <= args.prefill_tokens <= 24576 - 8:
+        ap.error("--prefill-tokens must lie in [1, 24568] (the 3B context is 24576)")
 
     import numpy as np
     import torch

@@ -327,6 +327,41 @@ def test_gemm_swiglu_epilogue(torch, yuear_lib, oracle, shape, m, n, k):
                                             dc.data_ptr(), n // 2, 2, shape, None) == 1
 
 
+def test_gemm_swiglu_every_gate_value(torch, yuear_lib, oracle):
+    """The GEMM's SwiGLU epilogue depends on the bf16 gate value alone (up
+    rounded apart), so all 65536 of them are checked (gate column i = bf16
+    bits i, up = 1, A = e_0): bit for bit against the decode GEMV's SwiGLU
+    (gemv_core.h) on every tile shape and through split-K's reduce kernel,
+    and against the oracle's silu_mul (ar.cpp:36-51) within the bf16 bound
+    for the finite ones."""
+    k, pairs = 128, 65536
+    a = np.zeros((1, k), np.uint16)
+    a[0, 0] = 0x3F80  # 1.0
+    w = np.zeros((2 * pairs, k), np.uint16)
+    w[0::2, 0] = np.arange(pairs, dtype=np.uint32).astype(np.uint16)
+    w[1::2, 0] = 0x3F80
+    da, dw = dev(torch, a), dev(torch, w)
+    dy = dev(torch, np.zeros((1, pairs), np.uint16))
+    assert yuear_lib.lib.yuear_op_gemv(dw.data_ptr(), 2 * pairs, k, 1, da.data_ptr(), k, None,
+                                       1e-5, dy.data_ptr(), pairs, 2, None) == 0
+    want = host(torch, dy)[0]
+    runs = [(shape, 1) for shape in range(6)] + [(4, 2)]
+    for shape, splits in runs:
+        dc = dev(torch, np.zeros((1, pairs), np.uint16))
+        assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), 1, 2 * pairs, k,
+                                                 dc.data_ptr(), pairs, 2, shape, splits,
+                                                 None) == 0
+        got = host(torch, dc)[0]
+        bad = np.flatnonzero(got != want)
+        print(f"shape {shape} splits {splits}: {bad.size} of {pairs} differ from the GEMV",
+              [(hex(int(i)), hex(int(got[i])), hex(int(want[i]))) for i in bad[:6]], flush=True)
+        assert bad.size == 0
+    gate = f(w[0::2, 0])
+    finite = np.isfinite(gate) & np.isfinite(f(want))
+    ref = oracle.silu_mul(w[0::2, 0][None, :], w[1::2, 0][None, :])[0]
+    assert_close_bf16(want[finite], ref[finite], scale=2.0 ** -100, exact_frac=0.99)
+
+
 @pytest.mark.parametrize("shape", range(6))
 @pytest.mark.parametrize("m,n,k,residual", [(300, 1000, 512, 0), (517, 776, 192, 1), (1, 200, 64, 1)])
 def test_gemm_every_tile_shape(torch, yuear_lib, oracle, shape, m, n, k, residual):
