@@ -449,6 +449,15 @@ def test_gemm_split_k_matches_oracle(torch, yuear_lib, oracle, m, n, k, residual
     assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), m, n, k,
                                              dev(torch, c0).data_ptr(), out_n, residual, 0, bad,
                                              None) == 1
+    # refused before any workspace is sized: a workspace beyond size_t, and K
+    # that is no whole number of 64-wide steps
+    huge = 1 << 30
+    assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), huge, huge, k,
+                                             dev(torch, c0).data_ptr(), huge, 0, 0, 2,
+                                             None) == 1
+    assert yuear_lib.lib.yuear_op_gemm_split(da.data_ptr(), k, dw.data_ptr(), m, n, k - 32,
+                                             dev(torch, c0).data_ptr(), out_n, residual, 0, 2,
+                                             None) == 1
 
 
 @pytest.mark.parametrize("m,n,k", [(7, 1024, 3072), (3000, 3072, 8192), (700, 5120, 3072)])

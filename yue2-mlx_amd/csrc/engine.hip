@@ -17,6 +17,7 @@
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -1863,7 +1864,10 @@ int32_t yuear_op_gemm_split(const uint16_t *a, int32_t lda, const uint16_t *w, i
   GemmParams p{a, lda, w, m, n, k, c, ldc, residual};
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (splits > 1) {
-    if (m < 1 || n < 1 || splits > 16)
+    // the checks launch_gemm_tile repeats, before anything is allocated
+    // (m * n below 2^58 keeps the workspace size within size_t)
+    if (m < 1 || n < 1 || splits > 16 || k < 64 || k % 64 || (k / 64) % splits ||
+        size_t(m) * size_t(n) > (SIZE_MAX >> 6))
       return int32_t(hipErrorInvalidValue);
     static OpPool pool;
     void *buf = nullptr;

@@ -568,7 +568,7 @@ int gemm_split_choice(int m, int n, int k, int shape, int cus, size_t part_bytes
     // whole 64-wide steps, at least 8 of them per split, the partials in the
     // workspace, no more workgroups than one round
     if ((k / kBK) % z || k / z < 8 * kBK || tiles * z > slots ||
-        size_t(z) * size_t(m) * size_t(n) * 4 > part_bytes)
+        size_t(m) * size_t(n) > part_bytes / (size_t(z) * 4))
       continue;
     best = z;
   }
@@ -580,7 +580,7 @@ hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int s
       !p.w || !p.c || p.residual < 0 || p.residual > 2 || (p.residual == 2 && p.n % 2) ||
       p.ldc < (p.residual == 2 ? p.n / 2 : p.n) || splits < 1 || splits > kMaxSplits ||
       (p.k / kBK) % splits ||
-      (splits > 1 && (!p.part || size_t(splits) * size_t(p.m) * size_t(p.n) * 4 > p.part_bytes)))
+      (splits > 1 && (!p.part || size_t(p.m) * size_t(p.n) > p.part_bytes / (size_t(splits) * 4))))
     return hipErrorInvalidValue;
   const bool sp = splits > 1;
   switch (shape) {
