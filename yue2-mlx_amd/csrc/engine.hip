@@ -91,9 +91,11 @@ const char *const kLayerNames[] = {"input_layernorm",  "post_attention_layernorm
                                    "mlp.gate_proj",    "mlp.up_proj",
                                    "mlp.down_proj"};
 constexpr int kNumLayerTensors = 11;
-// Split-K workspace of a session's prefill GEMMs: one round of 128 x 128
-// tiles on 256 CUs at two per CU (512 x 128 x 128 fp32) fits.
-constexpr size_t kSplitBytes = size_t(32) << 20;
+// Split-K workspace of a session's prefill GEMMs (fp32 partials, splits x
+// tokens x features): the largest split the plan picks at the 3B shape is
+// the down projection at 1024 tokens, 4 x 1024 x 3072 floats (48 MiB); a
+// split that does not fit is not considered.
+constexpr size_t kSplitBytes = size_t(64) << 20;
 
 int32_t tensor_id(const std::string &name) {
   if (name == "model.embed_tokens.weight") return 0;

@@ -554,25 +554,43 @@ int gemm_tile_choice(int m, int n, int cus) {
   return best;
 }
 
-int gemm_split_choice(int m, int n, int k, int shape, int cus, size_t part_bytes) {
-  if (shape < 0 || shape >= int(sizeof(kShapes) / sizeof(kShapes[0])) || m < 1 || n < 1)
-    return 1;
-  const TileShape &t = kShapes[shape];
-  const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
-  const long long slots = (long long)cus * t.per_cu;
-  // only grids that leave most of the GPU idle: K is then the serial chain
-  if (tiles * 4 > slots)
-    return 1;
-  int best = 1;
-  for (int z = 2; z <= kMaxSplits; ++z) {
-    // whole 64-wide steps, at least 8 of them per split, the partials in the
-    // workspace, no more workgroups than one round
-    if ((k / kBK) % z || k / z < 8 * kBK || tiles * z > slots ||
-        size_t(m) * size_t(n) > part_bytes / (size_t(z) * 4))
-      continue;
-    best = z;
+// Shape and split count together, by the tile model scaled to K / splits
+// steps, plus, for a split, the reduce kernel: 4 us and 0.4 us per MB it
+// moves (the splits' fp32 partials read, the bf16 result written) and 0.1 us
+// per MB of partials the tiles write instead of bf16 results. Fitted to
+// every (shape, splits) of the four 3B prefill projections at 128-2048
+// tokens on MI355X: the pick is within 9% of the fastest measured (split or
+// not) in all 28 cases; without a split it is gemm_tile_choice's shape.
+void gemm_plan(int m, int n, int k, int cus, size_t part_bytes, int *shape, int *splits) {
+  *shape = gemm_tile_choice(m, n, cus);
+  *splits = 1;
+  double best_t = 0;
+  const double mn = double(m) * double(n);
+  for (int i = 0; i < int(sizeof(kShapes) / sizeof(kShapes[0])); ++i) {
+    const TileShape &t = kShapes[i];
+    const long long tiles = (long long)((m + t.bm - 1) / t.bm) * ((n + t.bn - 1) / t.bn);
+    const long long slots = (long long)cus * t.per_cu;
+    for (int z = 1; z <= kMaxSplits; ++z) {
+      // whole 64-wide steps, at least 4 per split, the partials in the workspace
+      if ((k / kBK) % z || k / z < 4 * kBK ||
+          (z > 1 && size_t(m) * size_t(n) > part_bytes / (size_t(z) * 4)))
+        continue;
+      const long long wgs = tiles * z, full = wgs / slots, rem = wgs % slots;
+      double round = double(full) * t.round;
+      if (rem > cus)
+        round += t.round;
+      else if (rem > 0)
+        round += t.alone + (t.busy - t.alone) * double(rem) / cus;
+      double time = round * (double(k) / z / kBK) / 48.0;
+      if (z > 1)
+        time += 4.0 + 0.4e-6 * (4.0 * z * mn + 2.0 * mn) + 0.1e-6 * 4.0 * z * mn;
+      if ((i == 0 && z == 1) || time < best_t * 0.999) {
+        *shape = i;
+        *splits = z;
+        best_t = time;
+      }
+    }
   }
-  return best;
 }
 
 hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int splits) {
@@ -596,8 +614,9 @@ hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int s
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
   const int cus = device_cus();
-  const int shape = gemm_tile_choice(p.m, p.n, cus);
-  const int splits = p.part ? gemm_split_choice(p.m, p.n, p.k, shape, cus, p.part_bytes) : 1;
+  int shape = gemm_tile_choice(p.m, p.n, cus), splits = 1;
+  if (p.part)
+    gemm_plan(p.m, p.n, p.k, cus, p.part_bytes, &shape, &splits);
   return launch_gemm_tile(p, shape, s, splits);
 }
 

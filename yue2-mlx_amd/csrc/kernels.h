@@ -184,8 +184,8 @@ struct GemmParams {
   size_t part_bytes = 0;
 };
 // MFMA GEMM (gemm.hip); k a multiple of 64, lda a multiple of 8. With a
-// workspace it splits K over workgroups when the tiles alone leave most CUs
-// idle (gemm_split_choice), summing the splits in a fixed order.
+// workspace it may split K over workgroups (gemm_plan picks the tile shape
+// and split count together), summing the splits in a fixed order.
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
 // One of the GEMM's tile shapes (0..5, see gemm.hip) with K in `splits`
 // ranges (splits > 1 needs p.part of splits * m * n floats, k / 64 a multiple
@@ -193,7 +193,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
 // its split count.
 hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int splits = 1);
 int gemm_tile_choice(int m, int n, int cus);
-int gemm_split_choice(int m, int n, int k, int shape, int cus, size_t part_bytes);
+void gemm_plan(int m, int n, int k, int cus, size_t part_bytes, int *shape, int *splits);
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
                              int width, uint16_t *out, hipStream_t s);
