@@ -168,6 +168,31 @@ def test_repeated_runs_are_bit_identical(yuear_lib):
     engine.close()
 
 
+def test_prefill_fused_reduce_norm_is_bit_identical(yuear_lib, monkeypatch):
+    # A split residual GEMM (o_proj, down) and the RMSNorm after it run as one
+    # kernel (gemm_reduce_norm_kernel); YUEAR_PREFILL_FUSE_NORM=0 keeps the
+    # reduce kernel and the row norm apart. At the 3B layer shape both
+    # projections split at 100 and 700 tokens and down alone at 1024: prefill
+    # logits and the decode steps after it must be the same bits either way.
+    cfg = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=2,
+               num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=4096,
+               max_position_embeddings=4096, rms_norm_eps=1e-5, rope_theta=5e5, qk_norm=True)
+    engine = yuear_lib.Engine(cfg, seed=11)
+    rng = np.random.default_rng(11)
+    for n in (100, 700, 1024):
+        prompt = rng.integers(0, 4096, n).tolist()
+        toks = rng.integers(0, 4096, size=3)
+        runs = []
+        for fused in ("1", "0"):
+            monkeypatch.setenv("YUEAR_PREFILL_FUSE_NORM", fused)
+            s = engine.session(1, n + 8)
+            runs.append([s.prefill(0, prompt)] + [s.step(int(t))[0] for t in toks])
+            s.close()
+        for i, (a, b) in enumerate(zip(*runs)):
+            np.testing.assert_array_equal(a, b, err_msg=f"{n} tokens, output {i}")
+    engine.close()
+
+
 def test_chunked_prefill_is_bit_identical_to_one_pass(tiny):
     engine, _, _ = tiny
     ids = [5, 9, 14, 200, 33, 1, 511, 256, 3]

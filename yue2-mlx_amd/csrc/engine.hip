@@ -289,6 +289,9 @@ struct yuear_session {
   uint16_t *px = nullptr, *ph = nullptr, *pqkv = nullptr, *pq = nullptr, *pattn = nullptr,
            *pact = nullptr;
   float *psplit = nullptr;  // split-K partials of the prefill GEMMs (kSplitBytes)
+  // a split residual GEMM's reduce and the following RMSNorm in one kernel
+  // (YUEAR_PREFILL_FUSE_NORM=0: two kernels, the same results)
+  bool fuse_norm = true;
   int32_t *pids = nullptr;
   // host mirrors / pinned
   std::vector<int> host_pos;
@@ -639,6 +642,8 @@ void begin_session(yuear_session &S, yuear_engine *E, int branches, int capacity
     int splits = attn_decode_splits(branches, c.Hkv, S.kv_stride);
     if (const char *env = std::getenv("YUEAR_ATTN_SPLITS"))
       splits = std::atoi(env);
+    if (const char *env = std::getenv("YUEAR_PREFILL_FUSE_NORM"))
+      S.fuse_norm = std::atoi(env) != 0;
     S.max_splits = std::max(1, std::min({64, splits, S.kv_stride / attn::kBlock}));
   }
   const int G = c.Hq / c.Hkv;
@@ -947,9 +952,23 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
     std::memcpy(S.pin_tok, ids + start, size_t(T) * 4);
     HIPC(hipMemcpyAsync(S.pids, S.pin_tok, size_t(T) * 4, hipMemcpyHostToDevice, st));
     HIPC(launch_embed_rows(E.embed, S.pids, T, c.H, S.px, st));
+    // a residual projection into x, then (norm_w set) the RMSNorm of the
+    // updated rows into h: a split GEMM's reduce and the norm run as one
+    // kernel (bit-identical to the reduce kernel followed by the norm)
+    auto residual_then_norm = [&](GemmParams g, const uint16_t *norm_w) -> hipError_t {
+      int shape = 0, splits = 1;
+      gemm_plan(g.m, g.n, g.k, gemm_cus(), g.part_bytes, &shape, &splits);
+      const bool fuse = norm_w && splits > 1 && S.fuse_norm;
+      g.defer_reduce = fuse;
+      hipError_t e = launch_gemm_tile(g, shape, st, splits);
+      if (e != hipSuccess || !norm_w)
+        return e;
+      return fuse ? launch_gemm_reduce_norm(g, splits, norm_w, c.eps, S.ph, st)
+                  : launch_rms_norm_rows(S.px, T, c.H, norm_w, c.eps, S.ph, st);
+    };
+    HIPC(launch_rms_norm_rows(S.px, T, c.H, E.layers[0].input_ln, c.eps, S.ph, st));
     for (int l = 0; l < c.layers; ++l) {
       const LayerW &L = E.layers[l];
-      HIPC(launch_rms_norm_rows(S.px, T, c.H, L.input_ln, c.eps, S.ph, st));
       GemmParams g{S.ph, c.H, L.qkv, T, c.qkv(), c.H, S.pqkv, c.qkv(), 0, S.psplit, kSplitBytes};
       HIPC(launch_gemm(g, st));
       QkPrepParams qp;
@@ -984,13 +1003,14 @@ void prefill(yuear_session &S, int b, const int32_t *ids, int n, uint16_t *logit
       HIPC(launch_attn_prefill(ap, st));
       GemmParams og{S.pattn, c.Hq * c.D, L.o, T, c.H, c.Hq * c.D, S.px, c.H, 1, S.psplit,
                     kSplitBytes};
-      HIPC(launch_gemm(og, st));
-      HIPC(launch_rms_norm_rows(S.px, T, c.H, L.post_ln, c.eps, S.ph, st));
+      HIPC(residual_then_norm(og, L.post_ln));
       GemmParams gu{S.ph, c.H, L.gu, T, 2 * c.F, c.H, S.pact, c.F, 2, S.psplit,
                     kSplitBytes};  // SwiGLU epilogue
       HIPC(launch_gemm(gu, st));
+      // down + residual, then the next layer's input norm (the last layer's
+      // rows go to the final norm of the head)
       GemmParams dg{S.pact, c.F, L.down, T, c.H, c.F, S.px, c.H, 1, S.psplit, kSplitBytes};
-      HIPC(launch_gemm(dg, st));
+      HIPC(residual_then_norm(dg, l + 1 < c.layers ? E.layers[l + 1].input_ln : nullptr));
     }
     S.host_pos[b] += T;
     if (start + T >= n)  // final norm + projection of the last hidden row

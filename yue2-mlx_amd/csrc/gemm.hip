@@ -500,6 +500,85 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p, int spli
   }
 }
 
+// gemm_reduce_kernel's sum and residual epilogue for one row per workgroup,
+// then rms_norm_rows_kernel's RMSNorm of that row: the same 8-feature chunks
+// per thread (c = thread, thread + 256, ...), the same order of the squares'
+// sum, so x and y come out bit-identical to the two kernels. The row's new
+// values stay in registers (at most kNormChunks chunks per thread).
+constexpr int kNormChunks = 4;  // rows up to 8192 features
+__global__ __launch_bounds__(256) void gemm_reduce_norm_kernel(GemmParams p, int splits,
+                                                               const uint16_t *w, float eps,
+                                                               uint16_t *y) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = p.n / 8;
+  const size_t plane = size_t(p.m) * p.n;
+  u32x4 *xr = reinterpret_cast<u32x4 *>(p.c + size_t(r) * p.ldc);
+  uint32_t xn[kNormChunks][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int c = int(threadIdx.x) + 256 * i;
+    if (c >= chunks)
+      break;
+    const float *src = p.part + size_t(r) * p.n + 8 * c;
+    f32x4v a[kMaxSplits], b[kMaxSplits];
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < splits) {
+        a[z] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(src + z * plane));
+        b[z] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(src + z * plane + 4));
+      }
+    const u32x4 old = xr[c];
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < splits) {
+        v[0] += a[z].x;
+        v[1] += a[z].y;
+        v[2] += a[z].z;
+        v[3] += a[z].w;
+        v[4] += b[z].x;
+        v[5] += b[z].y;
+        v[6] += b[z].z;
+        v[7] += b[z].w;
+      }
+    const uint32_t oi[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xn[i][q] = pack_bf16x2(bflo(oi[q]) + rbf(v[2 * q]), bfhi(oi[q]) + rbf(v[2 * q + 1]));
+      const float lo = bflo(xn[i][q]), hi = bfhi(xn[i][q]);
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+    xr[c] = u32x4{xn[i][0], xn[i][1], xn[i][2], xn[i][3]};
+  }
+  ss = wave_sum(ss);
+  if (lane == 0)
+    red[wave] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float scale = rbf(1.0f / __builtin_sqrtf(total / float(p.n) + eps));
+  const u32x4 *g4 = reinterpret_cast<const u32x4 *>(w);
+  u32x4 *dst = reinterpret_cast<u32x4 *>(y + size_t(r) * p.n);
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int c = int(threadIdx.x) + 256 * i;
+    if (c >= chunks)
+      break;
+    const u32x4 g = g4[c];
+    const uint32_t gi[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = f2bf(rbf(bflo(xn[i][q]) * scale) * bflo(gi[q]));
+      const uint32_t hi = f2bf(rbf(bfhi(xn[i][q]) * scale) * bfhi(gi[q]));
+      o[q] = lo | (hi << 16);
+    }
+    dst[c] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 template <int BM, int BN, int WM, int WN>
 hipError_t launch_tile(void (*kern)(GemmParams, int, int), const GemmParams &p, int splits,
                        hipStream_t s) {
@@ -513,7 +592,7 @@ hipError_t launch_tile(void (*kern)(GemmParams, int, int), const GemmParams &p, 
   hipLaunchKernelGGL(kern, dim3(tiles, unsigned(splits)), dim3(WM * WN * 64), lds, s, p, tiles_n,
                      splits);
   e = hipGetLastError();
-  if (e != hipSuccess || splits == 1)
+  if (e != hipSuccess || splits == 1 || p.defer_reduce)
     return e;
   const size_t quads = size_t(p.m) * ((p.n + 3) / 4);
   const unsigned blocks = unsigned(std::min<size_t>((quads + 255) / 256, 4096));
@@ -611,6 +690,19 @@ hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int s
   }
   return hipErrorInvalidValue;
 }
+
+hipError_t launch_gemm_reduce_norm(const GemmParams &p, int splits, const uint16_t *norm_w,
+                                   float eps, uint16_t *y, hipStream_t s) {
+  if (p.m < 1 || p.n < 8 || p.n % 8 || p.n > 8 * 256 * kNormChunks || p.ldc != p.n ||
+      p.residual != 1 || !p.c || !p.part || !norm_w || !y || splits < 2 || splits > kMaxSplits ||
+      size_t(p.m) * size_t(p.n) > p.part_bytes / (size_t(splits) * 4))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(gemm_reduce_norm_kernel, dim3(p.m), dim3(256), 0, s, p, splits, norm_w, eps,
+                     y);
+  return hipGetLastError();
+}
+
+int gemm_cus() { return device_cus(); }
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t s) {
   const int cus = device_cus();

@@ -182,6 +182,8 @@ struct GemmParams {
   // split-K workspace: fp32 partials [splits][m][n]; null: K is never split
   float *part = nullptr;
   size_t part_bytes = 0;
+  // split-K: leave the partials to the caller's reduce (launch_gemm_reduce_norm)
+  bool defer_reduce = false;
 };
 // MFMA GEMM (gemm.hip); k a multiple of 64, lda a multiple of 8. With a
 // workspace it may split K over workgroups (gemm_plan picks the tile shape
@@ -193,6 +195,14 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t s);
 // its split count.
 hipError_t launch_gemm_tile(const GemmParams &p, int shape, hipStream_t s, int splits = 1);
 int gemm_tile_choice(int m, int n, int cus);
+int gemm_cus();  // CUs of the current device (256 if it cannot be read)
+// The reduce of a residual GEMM launched with defer_reduce and splits > 1
+// (c = bf16(c + bf16(sum of the splits in split order)), as
+// gemm_reduce_kernel) fused with the RMSNorm of the updated rows into y
+// (rms_norm_rows): one workgroup per row, bit-identical to the two kernels.
+// residual 1, n a multiple of 8 up to 8192, ldc == n.
+hipError_t launch_gemm_reduce_norm(const GemmParams &p, int splits, const uint16_t *norm_w,
+                                   float eps, uint16_t *y, hipStream_t s);
 void gemm_plan(int m, int n, int k, int cus, size_t part_bytes, int *shape, int *splits);
 
 hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows,
