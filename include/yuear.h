@@ -311,7 +311,8 @@ int32_t yuear_op_gemm_tile(const uint16_t *dev_a, int32_t lda, const uint16_t *d
  * floats, in a per-(device, stream) buffer that the first such call on a
  * stream allocates, so make it outside graph capture) that a second kernel
  * adds in split order before the epilogue: the form the engine's prefill
- * GEMMs take when their tiles alone leave most CUs idle. */
+ * GEMMs take where a time model of tile shape and split count picks it
+ * (short prompts; the down projection up to ~2048 tokens at the 3B shape). */
 int32_t yuear_op_gemm_split(const uint16_t *dev_a, int32_t lda, const uint16_t *dev_w,
                             int32_t m, int32_t n, int32_t k, uint16_t *dev_c,
                             int32_t ldc, int32_t residual, int32_t shape,
