@@ -240,7 +240,10 @@ yuear_status yuear_session_time_kernel(yuear_session *session,
  * arrival counters, the split-K GEMM's partials) is per (device, stream):
  * calls on different streams never share it. The first call on a stream (or
  * one needing a larger buffer) allocates, so make it outside graph capture;
- * yuear_op_gemm and yuear_op_gemm_tile use no scratch. ---- */
+ * yuear_op_gemm and yuear_op_gemm_tile use no scratch. The first SwiGLU
+ * GEMM (residual 2) on a device fills a 128 KiB silu table (one launch and a
+ * stream synchronisation): make it outside graph capture too, where it
+ * returns hipErrorStreamCaptureUnsupported. ---- */
 /* y[b][r] = bf16(x[b] . W[row(r)]) with optional RMSNorm prologue
  * (norm_w != NULL) and epilogue 0 store / 1 residual add / 2 SwiGLU pairs. */
 int32_t yuear_op_gemv(const uint16_t *dev_w, int32_t n, int32_t k,

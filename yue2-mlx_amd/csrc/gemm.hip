@@ -39,6 +39,7 @@
 // 256 tiles for 256 CUs where 256 x 192 leaves 64 CUs idle (down 148 -> 131
 // us, o_proj 61 -> 52).
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "kernels.h"
@@ -89,6 +90,38 @@ __device__ __forceinline__ void swiglu_store(const GemmParams &p, int m, int n, 
       c[0] = swiglu_one(v[0], v[1]);
     if (n + 3 < p.n)
       c[1] = swiglu_one(v[2], v[3]);
+  }
+}
+
+// silu(g) rounded to bf16 for every bf16 value g (index = g's bits), by the
+// expression swiglu_one evaluates: filled once per device (silu_table_kernel)
+// before the first SwiGLU launch that reads it.
+__device__ uint16_t g_silu_table[65536];
+constexpr int kSiluTableBytes = 65536 * 2;
+
+__global__ __launch_bounds__(256) void silu_table_kernel() {
+  const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+  const float g = bf2f(uint16_t(i));
+  g_silu_table[i] = f2bf(g * (1.0f / (1.0f + expf(-g))));
+}
+
+// swiglu_store with silu read from the table copy in LDS (`tab`): the same
+// bits as swiglu_one.
+__device__ __forceinline__ uint16_t swiglu_tab(const uint16_t *tab, float gate, float up) {
+  const float act = bf2f(tab[f2bf(gate)]);
+  return f2bf(act * rbf(up));
+}
+__device__ __forceinline__ void swiglu_store_tab(const GemmParams &p, const uint16_t *tab, int m,
+                                                 int n, const float *v) {
+  uint16_t *c = p.c + size_t(m) * p.ldc + (n >> 1);
+  if (n + 3 < p.n && (p.ldc & 1) == 0) {
+    *reinterpret_cast<uint32_t *>(c) =
+        uint32_t(swiglu_tab(tab, v[0], v[1])) | uint32_t(swiglu_tab(tab, v[2], v[3])) << 16;
+  } else {
+    if (n + 1 < p.n)
+      c[0] = swiglu_tab(tab, v[0], v[1]);
+    if (n + 3 < p.n)
+      c[1] = swiglu_tab(tab, v[2], v[3]);
   }
 }
 
@@ -410,6 +443,36 @@ __device__ __forceinline__ void gemm_tile16(const GemmParams &p, int tiles_n, in
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if (!SPLIT && p.residual == 2) {
+    // SwiGLU: the ring is free once every wave is past its last fragment
+    // reads; it takes the 128 KiB silu table (direct-to-LDS loads from the
+    // L2-resident global copy), and each pair's silu becomes one LDS read
+    // instead of an accurate exp and a division
+    __syncthreads();
+    const auto rt = rows_rsrc(g_silu_table, kSiluTableBytes);
+#pragma unroll
+    for (int i = 0; i < kSiluTableBytes / (NW * 1024); ++i) {
+      const int blk = i * NW + wave;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (lds_ptr_t)(gemm_lds + blk * 1024), 16,
+                                               uint32_t(blk * 1024 + lane * 16), 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): a barrier waits for no global load
+    __syncthreads();
+    const uint16_t *tab = reinterpret_cast<const uint16_t *>(gemm_lds);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * (BM / WM) + i * 16 + (lane & 15);
+      if (m >= p.m)
+        continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn * (BN / WN) + j * 16 + 4 * q4;
+        const float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        swiglu_store_tab(p, tab, m, n, v);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int m = m0 + wm * (BM / WM) + i * 16 + (lane & 15);
@@ -579,12 +642,47 @@ __global__ __launch_bounds__(256) void gemm_reduce_norm_kernel(GemmParams p, int
   }
 }
 
+// The global silu table of this device, filled on first use (one launch and
+// a synchronisation, so not inside a graph capture: refused there).
+hipError_t ensure_silu_table(hipStream_t s) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static bool done[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return e;
+  if (dev < 0 || dev >= kMaxDevices)
+    return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done[dev])
+    return hipSuccess;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess)
+    return e;
+  if (cs != hipStreamCaptureStatusNone)
+    return hipErrorStreamCaptureUnsupported;
+  hipLaunchKernelGGL(silu_table_kernel, dim3(65536 / 256), dim3(256), 0, s);
+  if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(s)) != hipSuccess)
+    return e;
+  done[dev] = true;
+  return hipSuccess;
+}
+
 template <int BM, int BN, int WM, int WN>
 hipError_t launch_tile(void (*kern)(GemmParams, int, int), const GemmParams &p, int splits,
                        hipStream_t s) {
-  const int lds = 2 * (BM + BN) * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  // the 16 x 16 x 32 tile bodies (all shapes but 128 x 128) read silu from an
+  // LDS table in a one-pass SwiGLU launch
+  constexpr bool kTile16 = !(BM == 128 && BN == 128);
+  const bool table = kTile16 && p.residual == 2 && splits == 1;
+  const int ring = 2 * (BM + BN) * 128;
+  const int lds = table ? std::max(ring, kSiluTableBytes) : ring;
+  hipError_t e = table ? ensure_silu_table(s) : hipSuccess;
+  if (e != hipSuccess)
+    return e;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e != hipSuccess)
     return e;
   const int tiles_n = (p.n + BN - 1) / BN;
