@@ -31,17 +31,29 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint16_t *table, 
     dst[c] = src[c];
 }
 
-// ar.cpp:30-35 per row.
+// ar.cpp:30-35 per row. Thread t takes the row's 8-feature chunks t, t + 256,
+// ... (at most kRowChunks, rows up to 8192 features), held in registers
+// between the squares' sum and the scaling (one read of the row).
+constexpr int kRowChunks = 4;
 __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const uint16_t *x, int width,
                                                             const uint16_t *w, float eps,
                                                             uint16_t *y) {
   __shared__ float red[4];
   const int r = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = width / 8;
   const u32x4 *src = reinterpret_cast<const u32x4 *>(x + size_t(r) * width);
+  u32x4 xv[kRowChunks];
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = int(threadIdx.x) + 256 * i;
+    xv[i] = c < chunks ? src[c] : u32x4{0u, 0u, 0u, 0u};
+  }
   float ss = 0.f;
-  for (int c = threadIdx.x; c < width / 8; c += 256) {
-    const u32x4 v = src[c];
-    const uint32_t vi[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    if (int(threadIdx.x) + 256 * i >= chunks)
+      break;
+    const uint32_t vi[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float lo = bflo(vi[q]), hi = bfhi(vi[q]);
@@ -56,9 +68,13 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const uint16_t *x, i
   const float scale = rbf(1.0f / __builtin_sqrtf(total / float(width) + eps));
   const u32x4 *g4 = reinterpret_cast<const u32x4 *>(w);
   u32x4 *dst = reinterpret_cast<u32x4 *>(y + size_t(r) * width);
-  for (int c = threadIdx.x; c < width / 8; c += 256) {
-    const u32x4 v = src[c], g = g4[c];
-    const uint32_t vi[4] = {v.x, v.y, v.z, v.w}, gi[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = int(threadIdx.x) + 256 * i;
+    if (c >= chunks)
+      break;
+    const u32x4 g = g4[c];
+    const uint32_t vi[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w}, gi[4] = {g.x, g.y, g.z, g.w};
     uint32_t o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -204,7 +220,7 @@ hipError_t launch_embed_rows(const uint16_t *table, const int32_t *ids, int rows
 
 hipError_t launch_rms_norm_rows(const uint16_t *x, int rows, int width, const uint16_t *w,
                                 float eps, uint16_t *y, hipStream_t s) {
-  if (rows < 1 || width % 8)
+  if (rows < 1 || width < 8 || width % 8 || width > 8 * 256 * kRowChunks)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(rms_norm_rows_kernel, dim3(rows), dim3(256), 0, s, x, width, w, eps, y);
   return hipGetLastError();
