@@ -128,11 +128,41 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(QkPrepParams p) {
       r[j].g0 = g.g0;
       r[j].g1 = g.g1;
     }
+    // norm_rope_apply's arithmetic for the 8 rows, with the per-row scale
+    // rbf(1 / sqrt(ssq / 128 + eps)) evaluated once for all rows (row j in
+    // lane j, read back as a scalar) instead of once per row across the
+    // wave, and the RoPE halves without a branch: lanes 0-31 add the
+    // negated partner product, which rounds to exactly minus the product
+    // (round-to-nearest-even is symmetric), so every result is the same bits
+    float x0[8], x1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      x0[j] = bflo(v[j]);
+      x1[j] = bfhi(v[j]);
+    }
+    if (gain != nullptr) {
+      float mine = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float ssq = wave_sum(x0[j] * x0[j] + x1[j] * x1[j]);
+        mine = lane == j ? ssq : mine;
+      }
+      const float sc_lane = rbf(1.0f / __builtin_sqrtf(mine / 128.0f + p.eps));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sc = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_lane), j));
+        x0[j] = rbf(rbf(x0[j] * sc) * r[j].g0);
+        x1[j] = rbf(rbf(x1[j] * sc) * r[j].g1);
+      }
+    }
+    const float sgn = lane < 32 ? -1.0f : 1.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int pos = base + j;
-      float y0, y1;
-      norm_rope_apply(bflo(v[j]), bfhi(v[j]), gain != nullptr, p.eps, r[j], lane, y0, y1);
+      const float p0 = sgn * xor32(x0[j], lane), p1 = sgn * xor32(x1[j], lane);
+      const float y0 = rbf(rbf(x0[j] * r[j].c0) + rbf(p0 * r[j].s0));
+      const float y1 = rbf(rbf(x1[j] * r[j].c1) + rbf(p1 * r[j].s1));
       if (pos < lo || pos >= hi)  // uniform per wave
         continue;
       uint32_t *dst =
