@@ -19,6 +19,8 @@
 // workgroups; both matter because a block step is a latency-bound chain
 // (MFMA accumulations, cross-lane max / sum, the exp2 and the P split).
 #pragma once
+#include <type_traits>
+
 #include "attn_core.h"
 #include "common.h"
 
@@ -273,7 +275,11 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
   fetch(b_lo * kBlock, b_lo % S);
   __builtin_amdgcn_s_waitcnt(0);  // (a barrier waits for no load)
   __syncthreads();
-  for (int b = b_lo; b < nblk; ++b) {
+  // one block; kMask: the causal / key-length mask, needed only from the
+  // first block with a key past the smallest kmax of the tile's queries (the
+  // blocks before it are visible to every query: same scores, no compares)
+  auto block = [&](int b, auto mask_tag) {
+    constexpr bool kMask = decltype(mask_tag)::value;
     const int stage = b % S, kb = b * kBlock;
     // block b + 1 into the stage every wave finished reading before the
     // previous barrier; in flight during this block's products
@@ -297,7 +303,8 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
     for (int T = 0; T < 2; ++T)
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        sc[4 * T + u] = kb + 8 * r + 4 * T + u <= kmax ? st[T][u] * qscale : -__builtin_inff();
+        sc[4 * T + u] = !kMask || kb + 8 * r + 4 * T + u <= kmax ? st[T][u] * qscale
+                                                                : -__builtin_inff();
     float mx = sc[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e)
@@ -340,7 +347,13 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of block b + 1
     __syncthreads();
-  }
+  };
+  const int kfull = (t.causal_pos >= 0 ? t.causal_pos + 1 : t.kv_len) / kBlock;
+  int b = b_lo;
+  for (; b < min(kfull, nblk); ++b)
+    block(b, std::false_type{});
+  for (; b < nblk; ++b)
+    block(b, std::true_type{});
   // lane (query 16 w + i, r) holds dims 16 dt + 4 r + [0, 4): out = bf16(o / l)
   const float L = sum_halves(sum_row_pairs(l_run));
   const int qi = 16 * wave + i;
