@@ -127,7 +127,7 @@ __device__ __forceinline__ void attn_query_tile(const QueryTile &t, float qscale
           for (int k = 0; k < 3; ++k) {
             const uint32_t u0 = __builtin_bit_cast(uint32_t, p0);
             const uint32_t u1 = __builtin_bit_cast(uint32_t, p1);
-            pw[k][q] = (u0 >> 16) | (u1 & 0xffff0000u);
+            pw[k][q] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);  // hi16(u0) | hi16(u1) << 16
             p0 -= __builtin_bit_cast(float, u0 & 0xffff0000u);
             p1 -= __builtin_bit_cast(float, u1 & 0xffff0000u);
           }
@@ -327,7 +327,7 @@ __device__ __forceinline__ void attn_query_tile64(const QueryTile &t, float qsca
       for (int k = 0; k < 3; ++k) {
         const uint32_t u0 = __builtin_bit_cast(uint32_t, p0);
         const uint32_t u1 = __builtin_bit_cast(uint32_t, p1);
-        pw[k][q] = (u0 >> 16) | (u1 & 0xffff0000u);
+        pw[k][q] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);  // hi16(u0) | hi16(u1) << 16
         p0 -= __builtin_bit_cast(float, u0 & 0xffff0000u);
         p1 -= __builtin_bit_cast(float, u1 & 0xffff0000u);
       }
